@@ -1,0 +1,206 @@
+"""Benchmark of the fused Cheby-RKV forward on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline]
+
+Default workload: BASELINE configs[1] ("headline"): B=4, S=16384, D=512
+(H=8, hd=64), K=8, fp32, static per-head lambda.  One step = one pass of
+the fused operator over one batch held in HBM.  Inputs rotate over 4
+buffer sets (>1 GB) so the 256 MB Infinity Cache cannot serve them.
+
+Prints ONE JSON line (rank 0).  ``roofline`` prices the dominant kernel
+against HBM: achieved = algorithmic bytes per launch (every input read once,
+every output written once) / average kernel duration measured with HIP
+events on the stream the kernel is launched on.  ``cpu_baseline`` times the
+CPU restatement of the reference's PyTorch path (oracle/reference_form.py)
+on this host's cores, on a bounded sample (one batch row).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from orthossm_amd import cheby_ema_forward, cheby_ema_ttt  # noqa: E402
+from orthossm_amd.synthetic import CONFIGS, make_config_inputs  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Clenshaw+EMA tokens/s and HBM GB/s (% of peak) at B=4 S=16K D=512, 1 GPU"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+
+
+def algorithmic_bytes(cfg) -> int:
+    """Compulsory bytes of one pass: x read + out written + coeffs, damping,
+    lambda, g (dynamic), EMA state in/out, grad (TTT)."""
+    esz = 2 if cfg.dtype == torch.bfloat16 else 4
+    n = cfg.B * cfg.S * cfg.D
+    total = 2 * n * esz
+    total += cfg.B * cfg.H * cfg.K * cfg.hd * 4          # coeffs
+    total += 2 * cfg.H * 4                               # damping, lambda
+    if cfg.dynamic:
+        total += cfg.B * cfg.S * cfg.H * 4               # g [B,S,H]
+    if cfg.chunk:
+        total += 2 * cfg.B * cfg.D * 4 * (cfg.S // cfg.chunk)   # state in/out per chunk
+    else:
+        total += cfg.B * cfg.D * 4                       # ema_final
+    if cfg.ttt:
+        total += cfg.B * cfg.H * cfg.K * cfg.hd * 4      # grad
+    return total
+
+
+def cpu_baseline(cfg):
+    """Reference-form CPU path on one batch row of the workload."""
+    from oracle import reference_form as RF
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    inp = make_config_inputs(cfg)
+    x = inp["x"][0:1].float()
+    c = inp["coeffs"][0:1]
+    S = min(cfg.S, 16384)
+    x = x[:, :S].contiguous()
+    RF.forward(x[:, :256], c, inp["damping"], inp["lam"])        # warm-up
+    times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        RF.forward(x, c, inp["damping"], inp["lam"])
+        times.append(time.perf_counter() - t0)
+    t = min(times)
+    tokens = S
+    return {
+        "value": tokens / t,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"one batch row of the workload: B=1 S={S} D={cfg.D} K={cfg.K} fp32, "
+                  f"basis+einsum+tanh and per-head EMA loop (oracle/reference_form.py), best of 2",
+        "gbs": algorithmic_bytes(cfg) / (cfg.B * cfg.S) * tokens / t / 1e9,
+        "cpu": platform.processor() or platform.machine(),
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def measured_traffic(workload: str):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f).get(workload)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="headline", choices=sorted(CONFIGS))
+    ap.add_argument("--sets", type=int, default=4, help="rotating input/output buffer sets")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only; the hot path shards over batch/heads with no "
+              "communication (see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    cfg = CONFIGS[args.workload]
+    dev = torch.device("cuda", 0)
+    inp = make_config_inputs(cfg)
+    x0 = inp["x"].to(dev)
+    c = inp["coeffs"].to(dev)
+    damp = inp["damping"].to(dev)
+    lam = inp["lam"].to(dev)
+    g = inp["g"].to(dev) if inp["g"] is not None else None
+    xs = [x0] + [x0.clone() for _ in range(args.sets - 1)]
+    outs = [torch.empty_like(x0) for _ in range(args.sets)]
+    del inp
+
+    def step(i):
+        x, out = xs[i % args.sets], outs[i % args.sets]
+        if cfg.ttt:
+            cheby_ema_ttt(x, c, damp, lam, g=g, out=out)
+        elif cfg.chunk:
+            state = None
+            for t0 in range(0, cfg.S, cfg.chunk):
+                _, state = cheby_ema_forward(x[:, t0:t0 + cfg.chunk], c, damp, lam, ema_init=state,
+                                             out=out[:, t0:t0 + cfg.chunk], return_state=True)
+        else:
+            cheby_ema_forward(x, c, damp, lam, g=g, out=out)
+
+    stream = torch.cuda.current_stream(dev)
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        step(i)
+        ev[i][1].record(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    per = sorted(a.elapsed_time(b) for a, b in ev)
+    med = per[len(per) // 2]
+    mean_kernel_ms = sum(per) / len(per)
+    ms_per_step = total_ms / args.steps
+    tokens = cfg.B * cfg.S
+    algo = algorithmic_bytes(cfg)
+    achieved_gbs = algo / (mean_kernel_ms * 1e-3) / 1e9
+
+    res = {
+        "metric": METRIC if args.workload == "headline" else f"Clenshaw+EMA tokens/s, workload {cfg.name}",
+        "value": tokens / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp32",
+        "data": "synthetic (seeded N(0,1) inputs, c_k ~ N(0,1/(k+1)^2))",
+        "config": {
+            "workload": f"BASELINE {cfg.name}: B={cfg.B} S={cfg.S} D={cfg.D} H={cfg.H} hd={cfg.hd} K={cfg.K} "
+                        f"{'bf16' if cfg.dtype == torch.bfloat16 else 'fp32'}"
+                        f"{' dynamic-lambda' if cfg.dynamic else ''}{' +TTT-grad' if cfg.ttt else ''}"
+                        f"{f' as {cfg.S // cfg.chunk} chunks with carry' if cfg.chunk else ''}",
+            "B": cfg.B, "S": cfg.S, "D": cfg.D, "H": cfg.H, "K": cfg.K,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved_gbs / HBM_PEAK_GBS,
+            "traffic": measured_traffic(args.workload),
+            "algorithmic_bytes": algo,
+            "kernel_ms_mean": mean_kernel_ms,
+            "kernel_ms_p10": per[len(per) // 10],
+            "kernel_ms_median": med,
+            "kernel_ms_p90": per[(9 * len(per)) // 10],
+        },
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(cfg)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

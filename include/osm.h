@@ -1,0 +1,132 @@
+/*
+ * osm.h — C ABI of the MI355X (gfx950) Cheby-RKV hot path.
+ *
+ * One fused operator, per batch b, token t, head h, lane j (d = h*hd + j):
+ *
+ *   u = x / (1 + |x|)                               softsign
+ *   p = sum_{k<K} c[b,h,k,j] T_k(u)                 Clenshaw, K <= 8
+ *   z = tanh(damping[h] * p)                        (z = 0 where x is NaN)
+ *   s[t] = lam[b,t,h] s[t-1] + (1 - lam[b,t,h]) z   s[-1] = ema_init (0 if NULL)
+ *   out  = clamp(s, -1, 1)                          (OSM_FLAG_NO_CLAMP disables)
+ *   lam[b,t,h] = lam_h, or clamp(lam_h + lam_shift * g[b,t,h], lam_min, lam_max)
+ *
+ * plus the test-time-training (TTT) coefficient gradient
+ *
+ *   L = mean_{b, t<S-1, d} (out[b,t,d] - y[b,t+1,d])^2,  y = x or softsign(x)
+ *   grad[b,h,k,j] = dL/dc[b,h,k,j] / (k+1)^2
+ *
+ * Reference interfaces replaced (paths relative to the OrthoSSM root):
+ *   osm_cheby_ema_fwd  the forward kernel launches
+ *                      _launch_ortho_megakernel (sdpc_kernel.py:2290-2344),
+ *                      the _EMAFastPathFn launch (sdpc_kernel.py:1661-1670) and
+ *                      the direct _fused_clenshaw_ema_kernel launch in
+ *                      precision_tests.py:47-73, with the EMA carry
+ *                      InitState/FinalState [B,D] (sdpc_kernel.py:1999-2003,
+ *                      2172-2177) exposed as ema_init / ema_final.
+ *   osm_cheby_ema_ttt  the coefficient-gradient chain of FusedChebyRKVv10.backward:
+ *                      _parallel_reverse_ema_kernel (sdpc_kernel.py:2463-2471),
+ *                      _parallel_backward_clenshaw_kernel_v10 (2487-2500) and
+ *                      grad_c_part.sum (2502), fused with the forward.
+ *
+ * Conventions
+ *   - All device pointers are caller-owned; the library allocates nothing.
+ *   - Launches are stream-ordered on `stream` (a hipStream_t passed as void*,
+ *     NULL = the null stream) and never synchronise the host.
+ *   - Returns OSM_OK (0) or a negative osm_status; osm_last_error() gives a
+ *     thread-local message.  Argument errors are detected before any HIP call.
+ *   - The workspace must be zero-filled before its first use (osm_workspace_init
+ *     or any zero fill).  Afterwards it keeps its own state between calls; two
+ *     calls that overlap in time must not share one workspace.
+ */
+#ifndef ORTHOSSM_AMD_OSM_H
+#define ORTHOSSM_AMD_OSM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OSM_ABI_VERSION 1
+#define OSM_MAX_K 8
+
+typedef enum osm_dtype { OSM_F32 = 0, OSM_BF16 = 1 } osm_dtype;
+
+typedef enum osm_status {
+  OSM_OK = 0,
+  OSM_E_ARG = -1,         /* NULL pointer, bad ABI version, bad flag */
+  OSM_E_SHAPE = -2,       /* dimension out of range or inconsistent */
+  OSM_E_DTYPE = -3,       /* unsupported dtype or dtype combination */
+  OSM_E_LAYOUT = -4,      /* misaligned pointer or stride */
+  OSM_E_WORKSPACE = -5,   /* workspace NULL, too small or misaligned */
+  OSM_E_HIP = -6          /* a HIP runtime call or kernel launch failed */
+} osm_status;
+
+/* flags */
+#define OSM_FLAG_NO_CLAMP 0x1 /* out = s instead of clamp(s, -1, 1) */
+
+/* TTT target y */
+typedef enum osm_ttt_target { OSM_TARGET_X = 0, OSM_TARGET_SOFTSIGN = 1 } osm_ttt_target;
+
+/*
+ * Operator arguments.  Strides are in elements.  The lane (last) dimension of
+ * x, out and coeffs is contiguous.  x and out rows start on 4-element
+ * boundaries: pointer aligned to 4 elements, x_stride_b/x_stride_s (and the
+ * out strides) multiples of 4.
+ */
+typedef struct osm_cheby_args {
+  int32_t abi_version;      /* = OSM_ABI_VERSION */
+  int32_t flags;            /* OSM_FLAG_* */
+  int64_t B, S, H, hd, K;   /* hd % 4 == 0, 1 <= K <= 8 */
+
+  const void* x;            /* [B,S,H*hd] of x_dtype */
+  int32_t x_dtype;
+  int64_t x_stride_b, x_stride_s;
+
+  void* out;                /* [B,S,H*hd] of out_dtype */
+  int32_t out_dtype;
+  int64_t out_stride_b, out_stride_s;
+
+  const float* coeffs;      /* [B,H,K,hd] fp32 */
+  int64_t c_stride_b, c_stride_h, c_stride_k;
+
+  const float* damping;     /* [H] fp32 */
+  const float* lam;         /* [H] fp32, the static per-head EMA decay */
+
+  const float* g;           /* optional [B,S,H] fp32; stride 0 broadcasts */
+  int64_t g_stride_b, g_stride_s, g_stride_h;
+  float lam_shift, lam_min, lam_max;
+
+  const float* ema_init;    /* optional [B, H*hd] fp32 contiguous */
+  float* ema_final;         /* optional [B, H*hd] fp32 contiguous */
+} osm_cheby_args;
+
+/* ABI version the library was built with (OSM_ABI_VERSION). */
+int osm_abi_version(void);
+
+/* Thread-local message of the last failing call on this thread ("" if none). */
+const char* osm_last_error(void);
+
+/* Workspace bytes needed by osm_cheby_ema_fwd (ttt = 0) or
+ * osm_cheby_ema_ttt (ttt = 1).  Reads only the shape fields, dtypes, K and
+ * whether g is NULL; returns 0 if those are invalid. */
+size_t osm_workspace_bytes(const osm_cheby_args* args, int ttt);
+
+/* Zero-fill `bytes` of workspace on `stream` with a fill kernel. */
+int osm_workspace_init(void* workspace, size_t bytes, void* stream);
+
+/* Fused forward.  Replaces the kernel launches listed in the header comment. */
+int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* Fused forward + TTT coefficient gradient.  `grad` is [B,H,K,hd] fp32
+ * contiguous and is overwritten.  `target` is an osm_ttt_target. */
+int osm_cheby_ema_ttt(const osm_cheby_args* args, float* grad, int target, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ORTHOSSM_AMD_OSM_H */

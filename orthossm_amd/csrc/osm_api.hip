@@ -1,0 +1,218 @@
+// C ABI of the Cheby-RKV hot path: argument validation, workspace sizing and
+// kernel dispatch.  Declared in include/osm.h.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "osm.h"
+#include "osm_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return OSM_OK;
+}
+
+struct Geometry {
+  int n_lbd = 0, n_lb = 0, n_tiles = 0;
+  bool dyn = false;
+  int kpad = 8;
+  bool empty = false;  // B == 0 or S == 0
+};
+
+bool aligned4(const void* p, int esize) { return ((uintptr_t)p % (uintptr_t)(4 * esize)) == 0; }
+
+// Validates `a` without touching the GPU and fills `geo` for the forward
+// (ttt = false, 256-token tiles) or the TTT kernel (128-token tiles).
+int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_only = false) {
+  if (!a) return fail(OSM_E_ARG, "args is NULL");
+  if (a->abi_version != OSM_ABI_VERSION)
+    return fail(OSM_E_ARG, "abi_version %d does not match library ABI %d", a->abi_version, OSM_ABI_VERSION);
+  if (a->flags & ~OSM_FLAG_NO_CLAMP) return fail(OSM_E_ARG, "unknown flag bits 0x%x", a->flags);
+  if (a->B < 0 || a->S < 0) return fail(OSM_E_SHAPE, "B=%lld and S=%lld must be >= 0", (long long)a->B, (long long)a->S);
+  if (a->H < 1 || a->hd < 4 || a->hd % 4 != 0)
+    return fail(OSM_E_SHAPE, "need H >= 1 and hd a positive multiple of 4 (H=%lld hd=%lld)", (long long)a->H,
+                (long long)a->hd);
+  if (a->K < 1 || a->K > OSM_MAX_K) return fail(OSM_E_SHAPE, "K=%lld outside [1, %d]", (long long)a->K, OSM_MAX_K);
+  const int64_t D = a->H * a->hd;
+  if (D > (int64_t(1) << 28)) return fail(OSM_E_SHAPE, "D=H*hd=%lld too large", (long long)D);
+  if (a->x_dtype != OSM_F32 && a->x_dtype != OSM_BF16) return fail(OSM_E_DTYPE, "x_dtype %d unsupported", a->x_dtype);
+  if (a->out_dtype != OSM_F32 && a->out_dtype != OSM_BF16)
+    return fail(OSM_E_DTYPE, "out_dtype %d unsupported", a->out_dtype);
+  geo->dyn = a->g != nullptr;
+  geo->kpad = a->K <= 4 ? 4 : 8;
+  geo->empty = a->B == 0 || a->S == 0;
+  if (geo->empty) return OSM_OK;
+  if (!shapes_only) {
+    if (!a->x || !a->out || !a->coeffs || !a->damping || !a->lam)
+      return fail(OSM_E_ARG, "x, out, coeffs, damping and lam must be non-NULL");
+    const int xs = a->x_dtype == OSM_F32 ? 4 : 2;
+    const int os = a->out_dtype == OSM_F32 ? 4 : 2;
+    if (!aligned4(a->x, xs) || a->x_stride_b % 4 || a->x_stride_s % 4 || a->x_stride_b < 0 || a->x_stride_s < 0)
+      return fail(OSM_E_LAYOUT, "x must be aligned to 4 elements with non-negative strides that are multiples of 4");
+    if (!aligned4(a->out, os) || a->out_stride_b % 4 || a->out_stride_s % 4 || a->out_stride_b < 0 ||
+        a->out_stride_s < 0)
+      return fail(OSM_E_LAYOUT,
+                  "out must be aligned to 4 elements with non-negative strides that are multiples of 4");
+    if (geo->dyn && !(a->lam_min <= a->lam_max))
+      return fail(OSM_E_ARG, "lam_min %g > lam_max %g", (double)a->lam_min, (double)a->lam_max);
+  }
+  const int64_t n_lbd = (D + 63) / 64;
+  const int64_t tile = ttt ? osm::kTileTTT : osm::kTile;
+  const int64_t n_tiles = (a->S + tile - 1) / tile;
+  const int64_t n_lb = a->B * n_lbd;
+  if (n_lb * n_tiles >= (int64_t(1) << 31) || a->S >= (int64_t(1) << 31) - osm::kTile)
+    return fail(OSM_E_SHAPE, "problem too large: %lld tiles", (long long)(n_lb * n_tiles));
+  geo->n_lbd = (int)n_lbd;
+  geo->n_lb = (int)n_lb;
+  geo->n_tiles = (int)n_tiles;
+  return OSM_OK;
+}
+
+osm::FwdParams make_params(const osm_cheby_args* a, const Geometry& geo, void* ws) {
+  osm::FwdParams p{};
+  p.x = a->x;
+  p.out = a->out;
+  p.coeffs = a->coeffs;
+  p.damping = a->damping;
+  p.lam = a->lam;
+  p.g = a->g;
+  p.ema_init = a->ema_init;
+  p.ema_final = a->ema_final;
+  p.hdr = reinterpret_cast<unsigned*>(ws);
+  p.slots = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + 256);
+  p.x_sb = a->x_stride_b;
+  p.x_ss = a->x_stride_s;
+  p.o_sb = a->out_stride_b;
+  p.o_ss = a->out_stride_s;
+  p.c_sb = a->c_stride_b;
+  p.c_sh = a->c_stride_h;
+  p.c_sk = a->c_stride_k;
+  p.g_sb = a->g_stride_b;
+  p.g_ss = a->g_stride_s;
+  p.g_sh = a->g_stride_h;
+  p.B = (int)a->B;
+  p.S = (int)a->S;
+  p.H = (int)a->H;
+  p.hd = (int)a->hd;
+  p.K = (int)a->K;
+  p.D = (int)(a->H * a->hd);
+  p.n_lbd = geo.n_lbd;
+  p.n_lb = geo.n_lb;
+  p.n_tiles = geo.n_tiles;
+  p.lam_shift = a->lam_shift;
+  p.lam_min = a->lam_min;
+  p.lam_max = a->lam_max;
+  p.clamp_out = (a->flags & OSM_FLAG_NO_CLAMP) ? 0 : 1;
+  return p;
+}
+
+size_t ws_bytes_for(const Geometry& geo, bool ttt, int K) {
+  if (geo.empty) return 256;
+  return ttt ? osm::ttt_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn, K)
+             : osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn);
+}
+
+int check_ws(const Geometry& geo, bool ttt, int K, void* ws, size_t ws_bytes) {
+  if (!ws) return fail(OSM_E_WORKSPACE, "workspace is NULL");
+  if ((uintptr_t)ws % 256) return fail(OSM_E_WORKSPACE, "workspace must be 256-byte aligned");
+  const size_t need = ws_bytes_for(geo, ttt, K);
+  if (ws_bytes < need)
+    return fail(OSM_E_WORKSPACE, "workspace has %zu bytes, needs %zu", ws_bytes, need);
+  return OSM_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(OSM_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// S == 0 (or B == 0): nothing to compute; the final state equals the initial one.
+int run_empty(const osm_cheby_args* a, hipStream_t stream) {
+  if (a->B > 0 && a->ema_final) {
+    const size_t n = (size_t)a->B * (size_t)(a->H * a->hd);
+    const hipError_t e = a->ema_init ? osm::launch_copy_state(a->ema_init, a->ema_final, n, stream)
+                                     : osm::launch_fill_zero(a->ema_final, n * sizeof(float), stream);
+    if (e != hipSuccess) return hip_fail(e, "state copy launch");
+  }
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int osm_abi_version(void) { return OSM_ABI_VERSION; }
+
+const char* osm_last_error(void) { return g_err.c_str(); }
+
+size_t osm_workspace_bytes(const osm_cheby_args* args, int ttt) {
+  Geometry geo;
+  if (check_args(args, &geo, ttt != 0, /*shapes_only=*/true) != OSM_OK) return 0;
+  return ws_bytes_for(geo, ttt != 0, (int)args->K);
+}
+
+int osm_workspace_init(void* workspace, size_t bytes, void* stream) {
+  if (!workspace) return fail(OSM_E_WORKSPACE, "workspace is NULL");
+  const hipError_t e = osm::launch_fill_zero(workspace, bytes, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "workspace fill launch");
+  return ok();
+}
+
+int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t workspace_bytes, void* stream) {
+  Geometry geo;
+  int rc = check_args(args, &geo, false);
+  if (rc != OSM_OK) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (geo.empty) return run_empty(args, st);
+  rc = check_ws(geo, false, (int)args->K, workspace, workspace_bytes);
+  if (rc != OSM_OK) return rc;
+  const osm::FwdParams p = make_params(args, geo, workspace);
+  const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, geo.kpad, st);
+  if (e != hipSuccess) return hip_fail(e, "forward kernel launch");
+  return ok();
+}
+
+int osm_cheby_ema_ttt(const osm_cheby_args* args, float* grad, int target, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  Geometry geo;
+  int rc = check_args(args, &geo, true);
+  if (rc != OSM_OK) return rc;
+  if (!grad && !geo.empty) return fail(OSM_E_ARG, "grad must be non-NULL");
+  if (target != OSM_TARGET_X && target != OSM_TARGET_SOFTSIGN)
+    return fail(OSM_E_ARG, "target %d is not an osm_ttt_target", target);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (geo.empty) {
+    if (args->B > 0 && grad) {
+      const size_t n = (size_t)args->B * args->H * args->K * args->hd;
+      const hipError_t e = osm::launch_fill_zero(grad, n * sizeof(float), st);
+      if (e != hipSuccess) return hip_fail(e, "grad fill launch");
+    }
+    return run_empty(args, st);
+  }
+  rc = check_ws(geo, true, (int)args->K, workspace, workspace_bytes);
+  if (rc != OSM_OK) return rc;
+  osm::FwdParams p = make_params(args, geo, workspace);
+  const size_t slot_bytes = osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn);
+  p.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((slot_bytes + 255) / 256) * 256);
+  p.ttt_scale = args->S > 1 ? (float)(2.0 / ((double)args->B * (double)(args->S - 1) * (double)p.D)) : 0.0f;
+  p.ttt_target = target;
+  const hipError_t e = osm::launch_ttt(p, grad, args->x_dtype, args->out_dtype, geo.dyn, geo.kpad, st);
+  if (e != hipSuccess) return hip_fail(e, "TTT kernel launch");
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,59 @@
+"""Drop-in replacement for the reference's public op ``apply_cheby_rkv_v10``.
+
+Reference: sdpc_kernel.py:2522-2606 (public op), alias
+``apply_cheby_rkv_core`` at sdpc_kernel.py:2610.
+
+Covered: the fixed-coefficient path the reference takes when
+``S < seq_threshold`` (``_fast_path_forward``, sdpc_kernel.py:1708-1744):
+stable softsign, Chebyshev evaluation, damping 0.98 - 0.06*h/H, tanh, EMA
+with the scalar momentum ``ema_momentum`` on every head, output clamp; the
+coefficients and momentum come back unchanged (cast to fp32, as
+sdpc_kernel.py:2549-2552).  The Chebyshev series is evaluated exactly
+(the reference's fast path also evaluates it exactly, by basis + einsum).
+
+Not covered yet: the full path with online Lion TTT over 256-token chunks
+(``FusedChebyRKVv10``, sdpc_kernel.py:2351-2515) and gradients through the
+op.  Both raise ``NotImplementedError`` instead of silently changing
+semantics.
+"""
+from __future__ import annotations
+
+import torch
+
+from .ops import cheby_ema_forward
+
+
+def v10_damping(n_heads: int, device=None) -> torch.Tensor:
+    """Per-head damping hard-coded in the reference kernels (sdpc_kernel.py:1734-1736)."""
+    h = torch.arange(n_heads, dtype=torch.float32, device=device)
+    return 0.98 - 0.06 * h / n_heads
+
+
+def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_momentum=0.9,
+                        lion_beta1=0.9, lion_beta2=0.99, lion_wd=0.01, chunk_size=256, use_bf16=False,
+                        gate_global=None, dynamic_lambda=None, use_lut=True, seq_threshold=384,
+                        lion_max_norm=14.0):
+    """Same signature and return convention as the reference:
+    returns (out [B,S,D] fp32, coeffs fp32, momentum_buf fp32 or None)."""
+    B, S, D = x.shape
+    if coeffs.dtype != torch.float32:
+        coeffs = coeffs.float()
+    if momentum_buf is not None and momentum_buf.dtype != torch.float32:
+        momentum_buf = momentum_buf.float()
+    if not (seq_threshold > 0 and S < seq_threshold):
+        raise NotImplementedError(
+            "orthossm_amd: the full path (online Lion TTT over chunks, S >= seq_threshold) is not "
+            "implemented; call with seq_threshold > S for the fixed-coefficient path, or use "
+            "orthossm_amd.cheby_ema_ttt for the fused TTT gradient.")
+    if torch.is_grad_enabled() and (x.requires_grad or coeffs.requires_grad):
+        raise NotImplementedError("orthossm_amd: gradients through apply_cheby_rkv_v10 are not implemented")
+    H = n_heads
+    if D % H:
+        raise ValueError(f"D={D} is not divisible by n_heads={H}")
+    damping = v10_damping(H, x.device)
+    lam = torch.full((H,), float(ema_momentum), dtype=torch.float32, device=x.device)
+    out = cheby_ema_forward(x, coeffs, damping, lam, out_dtype=torch.float32)
+    return out, coeffs, momentum_buf
+
+
+apply_cheby_rkv_core = apply_cheby_rkv_v10

@@ -1,0 +1,47 @@
+"""Shared helpers for the GPU parity tests (inputs, oracle calls, tolerances)."""
+import numpy as np
+import torch
+
+from oracle import cheby_ema as O
+from orthossm_amd.synthetic import make_inputs
+
+# fp32 tolerance of the spec: 1e-5 relative.  Checked two ways: normalised by
+# the largest reference magnitude, and elementwise with an absolute floor.
+RTOL = 1e-5
+ATOL = 1e-6
+
+
+def assert_close_fp32(got, want, rtol=RTOL, atol=ATOL, what="out"):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    both_nan = np.isnan(got) & np.isnan(want)
+    g, w = np.where(both_nan, 0.0, got), np.where(both_nan, 0.0, want)
+    assert not np.isnan(g).any(), f"{what}: NaN where the oracle has a number"
+    err = np.abs(g - w)
+    bad = err > rtol * np.abs(w) + atol
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - rtol * np.abs(w)), err.shape)
+        raise AssertionError(f"{what}: {bad.sum()} of {bad.size} elements off; worst at {i}: "
+                             f"got {g[i]!r} want {w[i]!r}; max rel {O.rel_err(g, w):.3e}")
+    assert O.rel_err(g, w) <= rtol, f"{what}: max-normalised error {O.rel_err(g, w):.3e}"
+
+
+def inputs(B, S, H, hd, K=8, seed=0, dynamic=False, dtype=torch.float32):
+    return make_inputs(B, S, H * hd, H, K, seed=seed, dynamic=dynamic, dtype=dtype)
+
+
+def to_dev(inp, dev):
+    return {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+
+
+def oracle_forward(inp, **kw):
+    g = inp.get("g")
+    return O.forward(inp["x"].double().numpy(), inp["coeffs"].numpy(), inp["damping"].numpy(),
+                     inp["lam"].numpy(), g=None if g is None else g.numpy(), **kw)
+
+
+def oracle_ttt(inp, **kw):
+    g = inp.get("g")
+    return O.ttt_grad(inp["x"].double().numpy(), inp["coeffs"].numpy(), inp["damping"].numpy(),
+                      inp["lam"].numpy(), g=None if g is None else g.numpy(), **kw)

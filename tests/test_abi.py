@@ -1,0 +1,126 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/osm.h declares, its struct layout matches the ctypes mirror, and
+argument errors come back as status codes before any HIP call."""
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from orthossm_amd import _native as nat
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "osm.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(osm_\w+)\s*\(", text)))
+
+
+def test_library_loads_with_matching_abi():
+    lib = nat.load()
+    assert lib.osm_abi_version() == nat.ABI_VERSION
+    assert lib.osm_last_error() == b""
+
+
+def test_every_declared_function_is_exported():
+    lib = nat.load()
+    declared = header_functions()
+    assert declared == sorted(nat.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_struct_layout_matches_ctypes():
+    fields = [f for f, _ in nat.ChebyArgs._fields_]
+    prog = ['#include <stdio.h>', '#include <stddef.h>', '#include "osm.h"', "int main(void){",
+            'printf("%zu\\n", sizeof(osm_cheby_args));']
+    prog += [f'printf("%zu\\n", offsetof(osm_cheby_args, {f}));' for f in fields]
+    prog += ["return 0;}"]
+    with tempfile.TemporaryDirectory() as d:
+        src, exe = os.path.join(d, "p.c"), os.path.join(d, "p")
+        open(src, "w").write("\n".join(prog))
+        subprocess.run(["gcc", "-std=c99", "-I", os.path.join(ROOT, "include"), src, "-o", exe], check=True)
+        vals = [int(v) for v in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
+    assert vals[0] == ctypes.sizeof(nat.ChebyArgs)
+    for f, off in zip(fields, vals[1:]):
+        assert getattr(nat.ChebyArgs, f).offset == off, f
+
+
+def _args(**kw):
+    a = nat.ChebyArgs()
+    a.abi_version = nat.ABI_VERSION
+    a.B, a.S, a.H, a.hd, a.K = 4, 16384, 8, 64, 8
+    a.x = a.out = a.coeffs = a.damping = a.lam = 0x10000   # never dereferenced: every case below is invalid
+    a.x_stride_b, a.x_stride_s = 16384 * 512, 512
+    a.out_stride_b, a.out_stride_s = 16384 * 512, 512
+    a.c_stride_b, a.c_stride_h, a.c_stride_k = 8 * 8 * 64, 8 * 64, 64
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_workspace_bytes_formula():
+    lib = nat.load()
+    a = _args()
+    # 256-byte header + one 8-byte word per (lane-block, 256-token tile, lane)
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 256 + 32 * 64 * 64 * 8
+    a.g = 0x10000
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 256 + 32 * 64 * 64 * 16
+    a.K = 9
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 0
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(abi_version=99), -1),
+    (dict(flags=0x100), -1),
+    (dict(K=0), -2),
+    (dict(K=9), -2),
+    (dict(hd=6), -2),
+    (dict(H=0), -2),
+    (dict(S=-1), -2),
+    (dict(x_dtype=7), -3),
+    (dict(out_dtype=2), -3),
+    (dict(x=0), -1),
+    (dict(x=0x10004), -4),          # not 16-byte aligned for fp32
+    (dict(x_stride_s=510), -4),
+    (dict(out_stride_b=-4), -4),
+])
+def test_argument_errors(kw, code):
+    lib = nat.load()
+    a = _args(**kw)
+    assert lib.osm_cheby_ema_fwd(ctypes.byref(a), None, 0, None) == code
+    assert lib.osm_last_error() != b""
+
+
+def test_workspace_errors():
+    lib = nat.load()
+    a = _args()
+    assert lib.osm_cheby_ema_fwd(ctypes.byref(a), None, 0, None) == -5
+    assert lib.osm_cheby_ema_fwd(ctypes.byref(a), ctypes.c_void_p(0x10000), 100, None) == -5
+    assert b"needs" in lib.osm_last_error()
+    assert lib.osm_cheby_ema_fwd(ctypes.byref(a), ctypes.c_void_p(0x10010), 1 << 30, None) == -5   # misaligned
+
+
+def test_ttt_argument_errors():
+    lib = nat.load()
+    a = _args()
+    assert lib.osm_cheby_ema_ttt(ctypes.byref(a), None, 0, None, 0, None) == -1        # grad NULL
+    assert lib.osm_cheby_ema_ttt(ctypes.byref(a), ctypes.c_void_p(0x10000), 5, None, 0, None) == -1  # target
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 1) > lib.osm_workspace_bytes(ctypes.byref(a), 0)
+
+
+def test_error_messages_are_thread_local():
+    import threading
+    lib = nat.load()
+    a = _args(K=9)
+    assert lib.osm_cheby_ema_fwd(ctypes.byref(a), None, 0, None) == -2
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(lib.osm_last_error()))
+    t.start()
+    t.join()
+    assert seen == [b""] and b"K=9" in lib.osm_last_error()

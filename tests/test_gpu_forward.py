@@ -1,0 +1,198 @@
+"""GPU parity of the fused forward (osm_cheby_ema_fwd through the C ABI)
+against the float64 oracle, at the BASELINE shapes and at edge cases."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close_fp32, inputs, oracle_forward, to_dev
+from oracle import cheby_ema as O
+from orthossm_amd import cheby_ema_forward
+from orthossm_amd.synthetic import CONFIGS, make_config_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def run(inp, dev, **kw):
+    d = to_dev(inp, dev)
+    res = cheby_ema_forward(d["x"], d["coeffs"], d["damping"], d["lam"], g=d.get("g"), **kw)
+    torch.cuda.synchronize()
+    return res
+
+
+def test_config0_cpu_reference_shape(dev):
+    inp = make_config_inputs(CONFIGS["cpu_ref"])
+    out, fin = run(inp, dev, return_state=True)
+    want, wfin = oracle_forward(inp)
+    assert_close_fp32(out.cpu(), want)
+    assert_close_fp32(fin.cpu(), wfin, what="ema_final")
+
+
+@pytest.mark.parametrize("B,S,H,hd,K", [
+    (1, 1, 8, 64, 8),        # one token
+    (2, 255, 8, 64, 8),      # one partial tile
+    (1, 257, 8, 64, 8),      # full tile + 1 token
+    (3, 1000, 4, 32, 5),     # hd < 64: two heads per lane-block, K padded to 8
+    (1, 300, 3, 20, 8),      # D = 60: partial lane-block
+    (2, 777, 2, 12, 3),      # D = 24, K <= 4 kernel
+    (1, 4096, 8, 64, 4),
+    (1, 64 * 256 + 77, 2, 32, 8),   # > 64 tiles: crosses a look-back checkpoint
+    (2, 3 * 64 * 256 + 5, 1, 64, 8),  # several checkpoints
+])
+def test_shapes(dev, B, S, H, hd, K):
+    inp = inputs(B, S, H, hd, K, seed=B * 1000 + S)
+    out, fin = run(inp, dev, return_state=True)
+    want, wfin = oracle_forward(inp)
+    assert_close_fp32(out.cpu(), want)
+    assert_close_fp32(fin.cpu(), wfin, what="ema_final")
+
+
+def test_special_values(dev):
+    inp = inputs(1, 600, 2, 32, 8, seed=3)
+    x = inp["x"]
+    specials = [0.0, -0.0, float("inf"), float("-inf"), float("nan"), 1e-42, -1e-42, 3e38, -3e38, 1e30, 1e-7]
+    for i, v in enumerate(specials):
+        x[0, 10 * i + 5, (7 * i) % 64] = v
+    x[0, 400:420, :] = float("nan")          # a run of NaN rows
+    out, fin = run(inp, dev, return_state=True)
+    want, wfin = oracle_forward(inp)
+    assert_close_fp32(out.cpu(), want)
+    assert_close_fp32(fin.cpu(), wfin, what="ema_final")
+
+
+def test_ema_init_carry_and_clamp(dev):
+    inp = inputs(2, 700, 8, 64, 8, seed=5)
+    init = torch.rand(2, 512) * 2 - 1
+    out, fin = run(inp, dev, ema_init=init.to(dev), return_state=True)
+    want, wfin = oracle_forward(inp, ema_init=init.numpy())
+    assert_close_fp32(out.cpu(), want)
+    assert_close_fp32(fin.cpu(), wfin, what="ema_final")
+    # |ema_init| > 1: output clamped, carried state not
+    big = torch.full((2, 512), 3.0)
+    out2, fin2 = run(inp, dev, ema_init=big.to(dev), return_state=True)
+    want2, wfin2 = oracle_forward(inp, ema_init=big.numpy())
+    assert_close_fp32(out2.cpu(), want2)
+    assert_close_fp32(fin2.cpu(), wfin2, what="ema_final")
+    out3 = run(inp, dev, ema_init=big.to(dev), clamp=False)
+    want3, _ = oracle_forward(inp, ema_init=big.numpy(), clamp_out=False)
+    assert_close_fp32(out3.cpu(), want3)
+
+
+@pytest.mark.parametrize("chunk", [1000, 256, 4096])
+def test_chunked_carry_equals_monolithic(dev, chunk):
+    inp = to_dev(inputs(1, 8192 + 300, 8, 64, 8, seed=9), dev)
+    mono, fm = cheby_ema_forward(inp["x"], inp["coeffs"], inp["damping"], inp["lam"], return_state=True)
+    state, outs = None, []
+    for t0 in range(0, inp["x"].shape[1], chunk):
+        o, state = cheby_ema_forward(inp["x"][:, t0:t0 + chunk], inp["coeffs"], inp["damping"], inp["lam"],
+                                     ema_init=state, return_state=True)
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert_close_fp32(torch.cat(outs, 1).cpu(), mono.cpu())
+    assert_close_fp32(state.cpu(), fm.cpu(), what="ema_final")
+
+
+@pytest.mark.parametrize("g_shape", ["BSH", "SH"])
+def test_dynamic_lambda(dev, g_shape):
+    inp = inputs(2, 3000, 8, 128, 8, seed=11, dynamic=True)
+    if g_shape == "SH":
+        inp["g"] = inp["g"][0].clone()
+    for shift in (0.004, 0.05):
+        out, fin = run(inp, dev, lam_shift=shift, return_state=True)
+        want, wfin = oracle_forward(inp, lam_shift=shift)
+        assert_close_fp32(out.cpu(), want)
+        assert_close_fp32(fin.cpu(), wfin, what="ema_final")
+
+
+@pytest.mark.parametrize("xdt,odt", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.bfloat16),
+                                     (torch.bfloat16, torch.float32)])
+def test_bf16_io(dev, xdt, odt):
+    inp = inputs(2, 2000, 8, 64, 8, seed=13, dtype=xdt)
+    out = run(inp, dev, out_dtype=odt)
+    assert out.dtype == odt
+    want, _ = oracle_forward(inp)
+    if odt == torch.float32:
+        assert_close_fp32(out.cpu(), want)
+    else:
+        # bf16 output: round-to-nearest-even of the fp32 result (spec: 2e-2 abs).
+        err = np.abs(out.float().cpu().numpy() - want)
+        assert err.max() <= 2e-2
+        assert np.all(err <= 2.0 ** -8 * np.abs(want) + 1e-6)
+
+
+def test_deterministic_and_workspace_reuse(dev):
+    """Results do not depend on timing: 20 launches on one workspace are
+    bitwise equal (covers the epoch tags and the header re-arm)."""
+    inp = to_dev(inputs(4, 16384, 8, 64, 8, seed=21, dynamic=True), dev)
+    ref = cheby_ema_forward(inp["x"], inp["coeffs"], inp["damping"], inp["lam"], g=inp["g"]).clone()
+    for _ in range(20):
+        o = cheby_ema_forward(inp["x"], inp["coeffs"], inp["damping"], inp["lam"], g=inp["g"])
+        assert torch.equal(o, ref)
+    # a different, smaller problem in between must not disturb the next one
+    small = to_dev(inputs(1, 1000, 2, 64, 4, seed=2), dev)
+    cheby_ema_forward(small["x"], small["coeffs"], small["damping"], small["lam"])
+    o = cheby_ema_forward(inp["x"], inp["coeffs"], inp["damping"], inp["lam"], g=inp["g"])
+    assert torch.equal(o, ref)
+
+
+def test_strided_input_view(dev):
+    inp = inputs(2, 500, 8, 64, 8, seed=17)
+    big = torch.randn(2, 1000, 512)
+    big[:, ::2] = inp["x"]
+    xv = big.to(dev)[:, ::2]                  # token stride 1024: no copy needed
+    d = to_dev(inp, dev)
+    out = cheby_ema_forward(xv, d["coeffs"], d["damping"], d["lam"])
+    want, _ = oracle_forward(inp)
+    assert_close_fp32(out.cpu(), want)
+
+
+def test_empty_sequence(dev):
+    inp = to_dev(inputs(2, 4, 8, 64, 8), dev)
+    init = torch.rand(2, 512, device=dev)
+    out, fin = cheby_ema_forward(inp["x"][:, :0], inp["coeffs"], inp["damping"], inp["lam"], ema_init=init,
+                                 return_state=True)
+    torch.cuda.synchronize()
+    assert out.shape == (2, 0, 512) and torch.equal(fin, init)
+
+
+def test_headline_config_full_size(dev):
+    """B=4 S=16384 D=512 fp32, against the oracle at full size."""
+    inp = make_config_inputs(CONFIGS["headline"])
+    out, fin = run(inp, dev, return_state=True)
+    want, wfin = oracle_forward(inp)
+    assert_close_fp32(out.cpu(), want)
+    assert_close_fp32(fin.cpu(), wfin, what="ema_final")
+
+
+def test_streaming_config_full_size(dev):
+    """B=1 S=262144 as 16 chunks of 16384 with EMA carry == one
+    monolithic scan, and the monolithic scan == oracle."""
+    cfg = CONFIGS["streaming"]
+    inp = make_config_inputs(cfg)
+    d = to_dev(inp, dev)
+    mono, fm = cheby_ema_forward(d["x"], d["coeffs"], d["damping"], d["lam"], return_state=True)
+    state, outs = None, []
+    for t0 in range(0, cfg.S, cfg.chunk):
+        o, state = cheby_ema_forward(d["x"][:, t0:t0 + cfg.chunk], d["coeffs"], d["damping"], d["lam"],
+                                     ema_init=state, return_state=True)
+        outs.append(o)
+    chunked = torch.cat(outs, 1).cpu()
+    mono = mono.cpu()
+    assert_close_fp32(chunked, mono)
+    assert_close_fp32(state.cpu(), fm.cpu(), what="ema_final")
+    want, wfin = oracle_forward(inp)
+    assert_close_fp32(mono, want)
+    assert_close_fp32(fm.cpu(), wfin, what="ema_final")
+
+
+def test_dynamic_config_full_size(dev):
+    """B=8 S=32768 D=1024 dynamic lambda.  The kernel runs at full
+    size; batches 0 and 7 are checked against the oracle (each batch row is
+    an independent recurrence)."""
+    inp = make_config_inputs(CONFIGS["dynamic"])
+    out, fin = run(inp, dev, return_state=True)
+    out, fin = out.cpu(), fin.cpu()
+    for b in (0, 7):
+        sub = {k: (v[b:b + 1] if k in ("x", "coeffs", "g") else v) for k, v in inp.items()}
+        want, wfin = oracle_forward(sub)
+        assert_close_fp32(out[b:b + 1], want)
+        assert_close_fp32(fin[b:b + 1], wfin, what="ema_final")

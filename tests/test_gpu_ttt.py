@@ -1,0 +1,104 @@
+"""GPU parity of the fused forward + TTT coefficient gradient
+(osm_cheby_ema_ttt through the C ABI) against the float64 adjoint oracle,
+itself pinned to torch autograd and finite differences."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close_fp32, inputs, oracle_forward, oracle_ttt, to_dev
+from oracle import cheby_ema as O
+from orthossm_amd import cheby_ema_forward, cheby_ema_ttt
+from orthossm_amd.synthetic import CONFIGS, make_config_inputs
+
+pytestmark = pytest.mark.gpu
+
+GRAD_RTOL = 1e-3   # spec tolerance for the gradient
+
+
+def run(inp, dev, **kw):
+    d = to_dev(inp, dev)
+    res = cheby_ema_ttt(d["x"], d["coeffs"], d["damping"], d["lam"], g=d.get("g"), **kw)
+    torch.cuda.synchronize()
+    return res
+
+
+def assert_grad(got, want, rtol=GRAD_RTOL):
+    got = got.cpu().double().numpy()
+    err = O.rel_err(got, want)
+    assert err <= rtol, f"grad max-normalised error {err:.3e}"
+    # per coefficient order as well, so a wrong 1/(k+1)^2 on a small k-slice shows
+    for k in range(want.shape[2]):
+        ek = O.rel_err(got[:, :, k], want[:, :, k])
+        assert ek <= 10 * rtol, f"grad[:, :, {k}] error {ek:.3e}"
+
+
+@pytest.mark.parametrize("B,S,H,hd,K,dyn,target", [
+    (1, 2048, 8, 64, 8, False, "x"),          # configs[0] shape
+    (2, 1000, 8, 64, 8, True, "x"),
+    (2, 777, 4, 32, 5, False, "softsign"),
+    (1, 300, 3, 20, 8, True, "x"),            # partial lane-block
+    (2, 129, 2, 64, 4, False, "x"),           # one token into the second tile
+    (1, 64 * 128 + 33, 1, 64, 8, False, "x"),  # crosses a look-back checkpoint
+    (3, 5000, 2, 16, 8, True, "softsign"),
+])
+def test_ttt_shapes(dev, B, S, H, hd, K, dyn, target):
+    inp = inputs(B, S, H, hd, K, seed=S + 7 * B, dynamic=dyn)
+    out, grad, fin = run(inp, dev, target=target, return_state=True)
+    G, want, wfin = oracle_ttt(inp, target=target)
+    assert_close_fp32(out.cpu(), want)
+    assert_close_fp32(fin.cpu(), wfin, what="ema_final")
+    assert_grad(grad, G)
+
+
+def test_ttt_tiny_sequences(dev):
+    for S in (1, 2, 3):
+        inp = inputs(2, S, 2, 8, 8, seed=S)
+        out, grad = run(inp, dev)
+        G, want, _ = oracle_ttt(inp)
+        assert_close_fp32(out.cpu(), want)
+        if S == 1:
+            assert torch.count_nonzero(grad) == 0
+        else:
+            assert_grad(grad, G)
+
+
+def test_ttt_with_carry_and_bf16(dev):
+    inp = inputs(2, 3000, 8, 64, 8, seed=31, dtype=torch.bfloat16)
+    init = torch.rand(2, 512) * 1.6 - 0.8
+    out, grad, fin = run(inp, dev, ema_init=init.to(dev), return_state=True)
+    G, want, wfin = oracle_ttt(inp, ema_init=init.numpy())
+    assert out.dtype == torch.bfloat16
+    err = np.abs(out.float().cpu().numpy() - want)
+    assert err.max() <= 2e-2 and np.all(err <= 2.0 ** -8 * np.abs(want) + 1e-6)
+    assert_close_fp32(fin.cpu(), wfin, what="ema_final")
+    assert_grad(grad, G)
+
+
+def test_ttt_forward_matches_forward_kernel(dev):
+    inp = to_dev(inputs(2, 5000, 8, 64, 8, seed=41, dynamic=True), dev)
+    o1 = cheby_ema_forward(inp["x"], inp["coeffs"], inp["damping"], inp["lam"], g=inp["g"])
+    o2, _ = cheby_ema_ttt(inp["x"], inp["coeffs"], inp["damping"], inp["lam"], g=inp["g"])
+    torch.cuda.synchronize()
+    assert_close_fp32(o2.cpu(), o1.cpu().double().numpy())
+
+
+def test_ttt_deterministic(dev):
+    inp = to_dev(inputs(4, 9000, 8, 64, 8, seed=43), dev)
+    o0, g0 = cheby_ema_ttt(inp["x"], inp["coeffs"], inp["damping"], inp["lam"])
+    for _ in range(10):
+        o, g = cheby_ema_ttt(inp["x"], inp["coeffs"], inp["damping"], inp["lam"])
+        assert torch.equal(o, o0) and torch.equal(g, g0)
+
+
+def test_bf16_ttt_config_full_size(dev):
+    """B=16 S=65536 D=512, bf16 I/O, fp32 state, fused TTT.  The
+    kernel runs at full size; batch 0's gradient is compared with the oracle
+    run on batch 0 alone (the MSE mean over B rows scales it by 1/B)."""
+    cfg = CONFIGS["bf16_ttt"]
+    inp = make_config_inputs(cfg)
+    out, grad = run(inp, dev)
+    sub = {k: (v[0:1] if k in ("x", "coeffs") else v) for k, v in inp.items()}
+    G, want, _ = oracle_ttt(sub)
+    err = np.abs(out[0:1].float().cpu().numpy() - want)
+    assert err.max() <= 2e-2
+    assert_grad(grad[0:1] * cfg.B, G)
