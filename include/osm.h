@@ -34,9 +34,15 @@
  *     NULL = the null stream) and never synchronise the host.
  *   - Returns OSM_OK (0) or a negative osm_status; osm_last_error() gives a
  *     thread-local message.  Argument errors are detected before any HIP call.
- *   - The workspace must be zero-filled before its first use (osm_workspace_init
- *     or any zero fill).  Afterwards it keeps its own state between calls; two
- *     calls that overlap in time must not share one workspace.
+ *   - The workspace (osm_workspace_bytes, 256-byte aligned) keeps state between
+ *     calls: a launch counter and tagged look-back words.  The library clears
+ *     it on the stream the first time it sees a workspace pointer (unless
+ *     osm_workspace_init zeroed it) and whenever the layout changes (shape,
+ *     K class, static/dynamic lambda, forward/TTT).  A workspace freed and a new
+ *     one allocated at the same address must be passed through
+ *     osm_workspace_init.  Two calls that overlap in time must not share one
+ *     workspace; if they do, every wave still exits (bounded waits) and the
+ *     header's fault word (offset 12) is set.
  */
 #ifndef ORTHOSSM_AMD_OSM_H
 #define ORTHOSSM_AMD_OSM_H

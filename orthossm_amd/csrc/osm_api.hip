@@ -3,7 +3,9 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
+#include <unordered_map>
 
 #include "osm.h"
 #include "osm_kernels.h"
@@ -140,6 +142,43 @@ int hip_fail(hipError_t e, const char* what) {
   return fail(OSM_E_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// Layout last used on each workspace.  Look-back words carry an epoch tag, so
+// a workspace can be reused without clearing as long as its layout is
+// unchanged; when the layout changes (other shape, mode or lambda kind) old
+// payloads could sit where the new layout expects tagged words, so the
+// workspace is cleared on the stream first.  A workspace seen for the first
+// time is cleared too, unless osm_workspace_init zeroed it.
+struct Layout {
+  int n_lb, n_tiles, kpad;
+  bool dyn, ttt;
+  bool operator==(const Layout& o) const {
+    return n_lb == o.n_lb && n_tiles == o.n_tiles && kpad == o.kpad && dyn == o.dyn && ttt == o.ttt;
+  }
+};
+const Layout kZeroed{-1, -1, -1, false, false};
+std::mutex g_ws_mu;
+std::unordered_map<uintptr_t, Layout> g_ws_layout;
+
+int prepare_workspace(void* ws, size_t need, const Geometry& geo, bool ttt, hipStream_t stream) {
+  const Layout now{geo.n_lb, geo.n_tiles, geo.kpad, geo.dyn, ttt};
+  bool clear;
+  {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    auto it = g_ws_layout.find((uintptr_t)ws);
+    clear = it == g_ws_layout.end() || !(it->second == now || it->second == kZeroed);
+    g_ws_layout[(uintptr_t)ws] = now;
+  }
+  if (clear) {
+    const hipError_t e = osm::launch_fill_zero(ws, need, stream);
+    if (e != hipSuccess) {
+      std::lock_guard<std::mutex> lk(g_ws_mu);
+      g_ws_layout.erase((uintptr_t)ws);
+      return hip_fail(e, "workspace clear launch");
+    }
+  }
+  return OSM_OK;
+}
+
 // S == 0 (or B == 0): nothing to compute; the final state equals the initial one.
 int run_empty(const osm_cheby_args* a, hipStream_t stream) {
   if (a->B > 0 && a->ema_final) {
@@ -167,8 +206,13 @@ size_t osm_workspace_bytes(const osm_cheby_args* args, int ttt) {
 
 int osm_workspace_init(void* workspace, size_t bytes, void* stream) {
   if (!workspace) return fail(OSM_E_WORKSPACE, "workspace is NULL");
+  if ((uintptr_t)workspace % 256 || bytes % 4) return fail(OSM_E_WORKSPACE, "workspace must be 256-byte aligned and a multiple of 4 bytes");
   const hipError_t e = osm::launch_fill_zero(workspace, bytes, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "workspace fill launch");
+  {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    g_ws_layout[(uintptr_t)workspace] = kZeroed;
+  }
   return ok();
 }
 
@@ -179,6 +223,8 @@ int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t worksp
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (geo.empty) return run_empty(args, st);
   rc = check_ws(geo, false, (int)args->K, workspace, workspace_bytes);
+  if (rc != OSM_OK) return rc;
+  rc = prepare_workspace(workspace, osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn), geo, false, st);
   if (rc != OSM_OK) return rc;
   const osm::FwdParams p = make_params(args, geo, workspace);
   const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, geo.kpad, st);
@@ -205,8 +251,12 @@ int osm_cheby_ema_ttt(const osm_cheby_args* args, float* grad, int target, void*
   }
   rc = check_ws(geo, true, (int)args->K, workspace, workspace_bytes);
   if (rc != OSM_OK) return rc;
-  osm::FwdParams p = make_params(args, geo, workspace);
+  // Only the header and look-back words need clearing: the TTT partials are
+  // fully written by every launch before they are read.
   const size_t slot_bytes = osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn);
+  rc = prepare_workspace(workspace, slot_bytes, geo, true, st);
+  if (rc != OSM_OK) return rc;
+  osm::FwdParams p = make_params(args, geo, workspace);
   p.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((slot_bytes + 255) / 256) * 256);
   p.ttt_scale = args->S > 1 ? (float)(2.0 / ((double)args->B * (double)(args->S - 1) * (double)p.D)) : 0.0f;
   p.ttt_target = target;

@@ -34,6 +34,7 @@ struct TileInfo {
   int tile, lb, b, lbd;
   unsigned epoch, tag_agg, tag_pre;
   bool is_last, is_ckpt;
+  bool valid;  // false only if the header was corrupted (ticket out of range)
 };
 
 // Thread coordinates inside the workgroup.
@@ -62,7 +63,10 @@ __device__ __forceinline__ TileInfo claim_tile(ChainLds& L, unsigned* hdr_words,
   }
   __syncthreads();
   TileInfo ti;
-  const int ticket = (int)L.ticket;
+  const unsigned raw = L.ticket;
+  ti.valid = raw < (unsigned)n_lb * (unsigned)n_tiles;
+  if (!ti.valid && threadIdx.x == 0) raise_fault(hdr_words);
+  const int ticket = ti.valid ? (int)raw : 0;
   ti.tile = ticket / n_lb;
   ti.lb = ticket - ti.tile * n_lb;
   ti.b = ti.lb / n_lbd;
@@ -130,7 +134,7 @@ __device__ __forceinline__ void tile_scan(ChainLds& L, const ThreadPos& q, const
 template <bool DYN, int R>
 __device__ __forceinline__ void look_back(ChainLds& L, const ThreadPos& q, const TileInfo& ti, float aggA,
                                           float aggB, const unsigned long long* lane_slots, size_t tile_stride,
-                                          float init_wl, float lam_static_wl) {
+                                          float init_wl, float lam_static_wl, unsigned* hdr_words) {
   if (ti.tile > 0) {
     const int g0 = (ti.tile / kCkpt) * kCkpt;
     const int beg = g0 + q.wave * kWPT;
@@ -152,9 +156,9 @@ __device__ __forceinline__ void look_back(ChainLds& L, const ThreadPos& q, const
       for (int i = 0; i < kWPT; ++i) {
         if (beg + i < end) {
           const unsigned long long* s = lane_slots + (size_t)(beg + i) * tile_stride;
-          const float Bp = await_word(s, vB[i], ti.tag_agg);
+          const float Bp = await_word(s, vB[i], ti.tag_agg, hdr_words);
           float Ap = Afull;
-          if constexpr (DYN) Ap = await_word(s + 1, vA[i], ti.tag_agg);
+          if constexpr (DYN) Ap = await_word(s + 1, vA[i], ti.tag_agg, hdr_words);
           mB = __builtin_fmaf(Ap, mB, Bp);
           mA *= Ap;
         }
@@ -168,7 +172,7 @@ __device__ __forceinline__ void look_back(ChainLds& L, const ThreadPos& q, const
         ck = init_wl;
       } else {
         const unsigned long long* s = lane_slots + (size_t)(g0 - 1) * tile_stride;
-        ck = await_word(s, peek(s), ti.tag_pre);
+        ck = await_word(s, peek(s), ti.tag_pre, hdr_words);
       }
     }
     __syncthreads();

@@ -30,13 +30,22 @@ constexpr float kTwoLog2e = 2.8853900817779268f;  // 2*log2(e): tanh via exp2
 //   ticket  next tile ticket of the running launch (reset to 0 by the last block)
 //   done    blocks finished in the running launch  (reset to 0 by the last block)
 //   epoch   launch counter; tags every published look-back word
+//   fault   set to 1 if a launch saw an out-of-range ticket or a look-back
+//           wait exceeded kSpinLimit (results of that launch are invalid);
+//           only a zero fill clears it
 struct WsHeader {
   unsigned ticket;
   unsigned done;
   unsigned epoch;
-  unsigned pad[61];
+  unsigned fault;
+  unsigned pad[60];
 };
 static_assert(sizeof(WsHeader) == 256, "header is 256 bytes");
+
+// Upper bound on polls of one look-back word (each poll is a device-scope
+// load plus a short sleep, so this is many seconds).  It only guarantees that
+// every wave exits even if the header was corrupted by overlapping calls.
+constexpr unsigned kSpinLimit = 1u << 24;
 
 // A look-back word is one 64-bit value: high 32 bits = (epoch << 2) | kind,
 // low 32 bits = an fp32 payload.  Because tag and payload travel in one
@@ -57,12 +66,22 @@ __device__ __forceinline__ unsigned long long peek(const unsigned long long* slo
   return __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+__device__ __forceinline__ void raise_fault(unsigned* hdr_words) {
+  __hip_atomic_store(hdr_words + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Spin until `slot` carries `tag`, starting from an already-loaded value.
 // The producer of every awaited word has a lower tile ticket, so it is
-// resident or finished and publishes without waiting on anyone: the loop ends.
-__device__ __forceinline__ float await_word(const unsigned long long* slot, unsigned long long w,
-                                            unsigned tag) {
+// resident or finished and publishes without waiting on anyone: the loop
+// ends.  kSpinLimit bounds it anyway (fault flag, payload 0).
+__device__ __forceinline__ float await_word(const unsigned long long* slot, unsigned long long w, unsigned tag,
+                                            unsigned* hdr_words) {
+  unsigned polls = 0;
   while ((unsigned)(w >> 32) != tag) {
+    if (++polls > kSpinLimit) {
+      raise_fault(hdr_words);
+      return 0.0f;
+    }
     __builtin_amdgcn_s_sleep(1);
     w = peek(slot);
   }

@@ -50,6 +50,10 @@ __global__ void __launch_bounds__(kThreads) cheby_ema_ttt_kernel(const FwdParams
 
   const ThreadPos q = thread_pos();
   const TileInfo ti = claim_tile(L, p.hdr, p.n_lb, p.n_lbd, p.n_tiles);
+  if (!ti.valid) {  // corrupted header: touch nothing, let the launch drain
+    finish_block(p.hdr, ti.epoch);
+    return;
+  }
   const int b = ti.b;
   const int d0 = ti.lbd * kLanes + q.l4 * kLPT;
   const bool lane_ok = d0 < p.D;
@@ -140,7 +144,7 @@ __global__ void __launch_bounds__(kThreads) cheby_ema_ttt_kernel(const FwdParams
   const bool dl_ok = dl < p.D;
   const float init_wl = (p.ema_init && dl_ok) ? p.ema_init[(int64_t)b * p.D + dl] : 0.0f;
   const float lam_wl = DYN ? 0.0f : p.lam[dl_ok ? dl / p.hd : 0];
-  look_back<DYN, R>(L, q, ti, aggA, aggB, lane_slots, tile_stride, init_wl, lam_wl);
+  look_back<DYN, R>(L, q, ti, aggA, aggB, lane_slots, tile_stride, init_wl, lam_wl, p.hdr);
 
   if (q.tg < kNTG - 1) {
 #pragma unroll

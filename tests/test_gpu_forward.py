@@ -66,15 +66,17 @@ def test_ema_init_carry_and_clamp(dev):
     want, wfin = oracle_forward(inp, ema_init=init.numpy())
     assert_close_fp32(out.cpu(), want)
     assert_close_fp32(fin.cpu(), wfin, what="ema_final")
-    # |ema_init| > 1: output clamped, carried state not
+    # |ema_init| > 1: output clamped, carried state not.  The state holds a
+    # 3*lam^t component that cancels against the z terms, so fp32 rounding is
+    # absolute in |init|: the absolute floor scales by 3.
     big = torch.full((2, 512), 3.0)
     out2, fin2 = run(inp, dev, ema_init=big.to(dev), return_state=True)
     want2, wfin2 = oracle_forward(inp, ema_init=big.numpy())
-    assert_close_fp32(out2.cpu(), want2)
-    assert_close_fp32(fin2.cpu(), wfin2, what="ema_final")
+    assert_close_fp32(out2.cpu(), want2, atol=3e-6)
+    assert_close_fp32(fin2.cpu(), wfin2, atol=3e-6, what="ema_final")
     out3 = run(inp, dev, ema_init=big.to(dev), clamp=False)
     want3, _ = oracle_forward(inp, ema_init=big.numpy(), clamp_out=False)
-    assert_close_fp32(out3.cpu(), want3)
+    assert_close_fp32(out3.cpu(), want3, atol=3e-6)
 
 
 @pytest.mark.parametrize("chunk", [1000, 256, 4096])
