@@ -103,6 +103,9 @@ def main():
     ap.add_argument("--workload", default="headline", choices=sorted(CONFIGS))
     ap.add_argument("--sets", type=int, default=4, help="rotating input/output buffer sets")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="after the timed steps, run 5 plain device copies of one x buffer (reads and writes "
+                         "B*S*D elements each) as the reference kernel for HBM counter scaling")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -197,6 +200,11 @@ def main():
             "kernel_ms_p90": per[(9 * len(per)) // 10],
         },
     }
+    if args.calibrate_copy:
+        for i in range(5):
+            outs[i % args.sets].copy_(xs[(i + 1) % args.sets])
+        torch.cuda.synchronize()
+        res["copy_calibration_bytes_each_way"] = xs[0].numel() * xs[0].element_size()
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(cfg)
     print(json.dumps(res), flush=True)

@@ -30,7 +30,7 @@ int ok() {
 }
 
 struct Geometry {
-  int n_lbd = 0, n_lb = 0, n_tiles = 0;
+  int n_lbd = 0, n_lb = 0, n_lb_pad = 0, n_tiles = 0;
   bool dyn = false;
   int kpad = 8;
   bool empty = false;  // B == 0 or S == 0
@@ -72,15 +72,36 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
                   "out must be aligned to 4 elements with non-negative strides that are multiples of 4");
     if (geo->dyn && !(a->lam_min <= a->lam_max))
       return fail(OSM_E_ARG, "lam_min %g > lam_max %g", (double)a->lam_min, (double)a->lam_max);
+    // Rows of out must not overlap (padding rows of the last tile are masked
+    // by extent, which needs out_stride_s >= D and batches after all rows).
+    if (a->out_stride_s < D || a->out_stride_b < a->S * a->out_stride_s)
+      return fail(OSM_E_LAYOUT, "out rows/batches overlap (out_stride_s=%lld < D or out_stride_b too small)",
+                  (long long)a->out_stride_s);
+    // One tile's byte span must fit a buffer descriptor's 31-bit offsets.
+    const int64_t tile_rows = osm::FwdGeo::TILE > osm::TttGeo::TILE ? osm::FwdGeo::TILE : osm::TttGeo::TILE;
+    if ((tile_rows * a->x_stride_s + D) * xs >= (int64_t(1) << 31) ||
+        (tile_rows * a->out_stride_s + D) * os >= (int64_t(1) << 31))
+      return fail(OSM_E_LAYOUT, "token stride too large for 31-bit tile offsets");
+    if (geo->dyn) {
+      if (a->g_stride_b < 0 || a->g_stride_s < 0 || a->g_stride_h < 0)
+        return fail(OSM_E_LAYOUT, "g strides must be non-negative");
+      if ((tile_rows * a->g_stride_s + a->H * a->g_stride_h + 1) * 4 >= (int64_t(1) << 31))
+        return fail(OSM_E_LAYOUT, "g strides too large for 31-bit tile offsets");
+    }
+    if ((a->H * a->c_stride_h + a->K * a->c_stride_k + a->hd) * 4 >= (int64_t(1) << 31) || a->c_stride_h < 0 ||
+        a->c_stride_k < 0 || a->c_stride_b < 0)
+      return fail(OSM_E_LAYOUT, "coeffs strides must be non-negative and fit 31-bit offsets");
   }
   const int64_t n_lbd = (D + 63) / 64;
-  const int64_t tile = ttt ? osm::kTileTTT : osm::kTile;
+  const int64_t tile = ttt ? osm::TttGeo::TILE : osm::FwdGeo::TILE;
   const int64_t n_tiles = (a->S + tile - 1) / tile;
   const int64_t n_lb = a->B * n_lbd;
-  if (n_lb * n_tiles >= (int64_t(1) << 31) || a->S >= (int64_t(1) << 31) - osm::kTile)
+  const int64_t n_lb_pad = (n_lb + 7) / 8 * 8;
+  if (n_lb_pad * n_tiles >= (int64_t(1) << 31) || a->S >= (int64_t(1) << 31) - tile)
     return fail(OSM_E_SHAPE, "problem too large: %lld tiles", (long long)(n_lb * n_tiles));
   geo->n_lbd = (int)n_lbd;
   geo->n_lb = (int)n_lb;
+  geo->n_lb_pad = (int)n_lb_pad;
   geo->n_tiles = (int)n_tiles;
   return OSM_OK;
 }
@@ -96,7 +117,7 @@ osm::FwdParams make_params(const osm_cheby_args* a, const Geometry& geo, void* w
   p.ema_init = a->ema_init;
   p.ema_final = a->ema_final;
   p.hdr = reinterpret_cast<unsigned*>(ws);
-  p.slots = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + 256);
+  p.slots = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + osm::kHeaderBytes);
   p.x_sb = a->x_stride_b;
   p.x_ss = a->x_stride_s;
   p.o_sb = a->out_stride_b;
@@ -115,6 +136,7 @@ osm::FwdParams make_params(const osm_cheby_args* a, const Geometry& geo, void* w
   p.D = (int)(a->H * a->hd);
   p.n_lbd = geo.n_lbd;
   p.n_lb = geo.n_lb;
+  p.n_lb_pad = geo.n_lb_pad;
   p.n_tiles = geo.n_tiles;
   p.lam_shift = a->lam_shift;
   p.lam_min = a->lam_min;
@@ -124,7 +146,7 @@ osm::FwdParams make_params(const osm_cheby_args* a, const Geometry& geo, void* w
 }
 
 size_t ws_bytes_for(const Geometry& geo, bool ttt, int K) {
-  if (geo.empty) return 256;
+  if (geo.empty) return osm::kHeaderBytes;
   return ttt ? osm::ttt_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn, K)
              : osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn);
 }

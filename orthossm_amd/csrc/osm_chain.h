@@ -1,4 +1,4 @@
-// Tile chaining protocol shared by the fused kernels: ticketed tiles, the
+// Tile chaining protocol shared by the fused kernels: tile assignment, the
 // token-group scan inside a tile, and the single-pass checkpointed look-back
 // that hands each tile its EMA carry-in.
 //
@@ -11,6 +11,23 @@
 // Every tile publishes its aggregate except the last tile of a group, which
 // publishes its inclusive state as the next checkpoint.  The composition
 // order is fixed, so results do not depend on timing.
+//
+// Tile order.  Virtual tile v covers tile v / n_lb_pad of lane-block
+// v % n_lb_pad, with n_lb_pad = n_lb rounded up to a multiple of 8 (virtual
+// tiles with lane-block >= n_lb are padding and are skipped).  A tile waits
+// only on earlier tiles of its lane-block: v - k*n_lb_pad, the same class
+// v % 8.  Two ways of handing out tiles keep every awaited tile with a
+// producer that already runs:
+//   * persistent (forward kernel): each class has a ticket counter; a block
+//     of class blockIdx % 8 takes tickets of its class one at a time
+//     (ticket_to_tile).  A ticket is taken by a running block, and every
+//     tile a block waits on has a smaller ticket of the same class, so its
+//     producer is running or done: no assumption on dispatch order or
+//     co-residency.
+//   * one tile per block (TTT kernel): block b handles v = b.  Awaited blocks
+//     have a lower index at a stride that is a multiple of 8; workgroups go
+//     to the 8 XCDs round-robin by index and in index order within an XCD,
+//     so each awaited block sits on the same XCD and was dispatched first.
 #pragma once
 
 #include "osm_device.h"
@@ -18,77 +35,96 @@
 
 namespace osm {
 
-constexpr int kNTG = kWaves * kTGW;   // 16 token groups per tile
-constexpr int kWPT = kCkpt / kWaves;  // look-back words read per thread
-
+template <class G>
 struct ChainLds {
-  unsigned ticket, epoch;
-  float A[kNTG][kTPR];        // token-group aggregate A (one per thread = per 4 lanes)
-  float B[kNTG][kLanes];      // token-group aggregate B per lane
-  float mA[kWaves][kLanes];   // look-back partial maps per wave
-  float mB[kWaves][kLanes];
-  float carry[kLanes];        // resolved carry-in of the tile
+  float A[G::NTG][G::TPR];      // token-group aggregate A (one per thread)
+  float B[G::NTG][kLanes];      // token-group aggregate B per lane
+  float mA[G::WAVES][kLanes];   // look-back partial maps per wave
+  float mB[G::WAVES][kLanes];
+  float carry[kLanes];          // resolved carry-in of the tile
+  int next_v;                   // broadcast of the next ticket (persistent kernels)
 };
 
 struct TileInfo {
-  int tile, lb, b, lbd;
-  unsigned epoch, tag_agg, tag_pre;
+  int v, tile, lb, b, lbd;
   bool is_last, is_ckpt;
-  bool valid;  // false only if the header was corrupted (ticket out of range)
+  bool pad;  // padding tile: no lane-block
 };
 
-// Thread coordinates inside the workgroup.
+struct Tags {
+  unsigned epoch, agg, pre;
+};
+
+// Thread coordinates inside the workgroup: wave, lane in wave (wl), thread in
+// its 64-lane row (lt: lanes lt*LPT .. lt*LPT+LPT-1) and token group (tg).
 struct ThreadPos {
-  int tid, wave, wl, l4, tg;
+  int tid, wave, wl, lt, tg;
 };
 
+template <class G>
 __device__ __forceinline__ ThreadPos thread_pos() {
   ThreadPos q;
   q.tid = threadIdx.x;
   q.wave = q.tid >> 6;
   q.wl = q.tid & 63;
-  q.l4 = q.wl & (kTPR - 1);
-  q.tg = q.wave * kTGW + (q.wl >> 4);
+  q.lt = q.wl % G::TPR;
+  q.tg = q.wave * G::TGW + q.wl / G::TPR;
   return q;
 }
 
-// Thread 0 takes the next ticket; tickets are handed out in start order, so
-// all tiles with a lower ticket are resident or finished.
-__device__ __forceinline__ TileInfo claim_tile(ChainLds& L, unsigned* hdr_words, int n_lb, int n_lbd,
-                                               int n_tiles) {
-  WsHeader* hdr = reinterpret_cast<WsHeader*>(hdr_words);
-  if (threadIdx.x == 0) {
-    L.ticket = __hip_atomic_fetch_add(&hdr->ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    L.epoch = __hip_atomic_load(&hdr->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
+// Launch epoch: constant for the whole launch (the last block bumps it only
+// after every block of this launch has read it).
+__device__ __forceinline__ Tags launch_tags(unsigned* hdr_words) {
+  Tags t;
+  t.epoch = __hip_atomic_load(hdr_words, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  t.agg = make_tag(t.epoch, kKindAgg);
+  t.pre = make_tag(t.epoch, kKindPre);
+  return t;
+}
+
+__device__ __forceinline__ TileInfo tile_info(int v, int n_lb, int n_lb_pad, int n_lbd, int n_tiles) {
   TileInfo ti;
-  const unsigned raw = L.ticket;
-  ti.valid = raw < (unsigned)n_lb * (unsigned)n_tiles;
-  if (!ti.valid && threadIdx.x == 0) raise_fault(hdr_words);
-  const int ticket = ti.valid ? (int)raw : 0;
-  ti.tile = ticket / n_lb;
-  ti.lb = ticket - ti.tile * n_lb;
+  ti.v = v;
+  ti.tile = v / n_lb_pad;
+  ti.lb = v - ti.tile * n_lb_pad;
+  ti.pad = ti.lb >= n_lb;
   ti.b = ti.lb / n_lbd;
   ti.lbd = ti.lb - ti.b * n_lbd;
-  ti.epoch = L.epoch;
-  ti.tag_agg = make_tag(ti.epoch, kKindAgg);
-  ti.tag_pre = make_tag(ti.epoch, kKindPre);
   ti.is_last = ti.tile == n_tiles - 1;
   ti.is_ckpt = (ti.tile % kCkpt) == kCkpt - 1;
   return ti;
 }
 
-// Aggregate A of a full tile of R-token runs under a static lambda, in the
-// same multiplication order as the producing workgroup's scan.
-template <int R>
+__device__ __forceinline__ unsigned take_ticket(unsigned* hdr_words, int cls) {
+  WsHeader* hdr = reinterpret_cast<WsHeader*>(hdr_words);
+  return __hip_atomic_fetch_add(&hdr->cls[cls].ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Lane-blocks of class cls (lb % 8 == cls, lb < n_lb).
+__device__ __forceinline__ int class_lane_blocks(int cls, int n_lb) { return cls < n_lb ? (n_lb - cls + 7) / 8 : 0; }
+
+// Virtual tile v = tile * n_lb_pad + lb of ticket k of class cls: tickets
+// walk the class's lane-blocks fastest, then tiles, so ticket k waits only
+// on tickets k - m, k - 2m, ... (m lane-blocks in the class).  Returns
+// n_virt when the class is exhausted.
+__device__ __forceinline__ int ticket_to_tile(unsigned k, int cls, int n_lb, int n_lb_pad, int n_tiles) {
+  const int m = class_lane_blocks(cls, n_lb);
+  if (m == 0 || (int)k >= m * n_tiles) return n_lb_pad * n_tiles;
+  const int tile = (int)k / m;
+  const int lb = cls + 8 * ((int)k - tile * m);
+  return tile * n_lb_pad + lb;
+}
+
+// Aggregate A of a full tile under a static lambda, in the same
+// multiplication order as the producing workgroup's scan.
+template <class G>
 __device__ __forceinline__ float static_tile_A(float lam) {
   float a = 1.0f;
 #pragma unroll
-  for (int r = 0; r < R; ++r) a *= lam;
+  for (int r = 0; r < G::R; ++r) a *= lam;
   float A = 1.0f;
 #pragma unroll
-  for (int q = 0; q < kNTG; ++q) A *= a;
+  for (int q = 0; q < G::NTG; ++q) A *= a;
   return A;
 }
 
@@ -96,69 +132,89 @@ __device__ __forceinline__ float static_tile_A(float lam) {
 // mapping the tile carry to the state before this thread's first token; in
 // wave 0, (aggA, aggB) = the tile aggregate of lane wl, which is published
 // unless the tile is a checkpoint or the last tile.
-template <bool DYN>
-__device__ __forceinline__ void tile_scan(ChainLds& L, const ThreadPos& q, const TileInfo& ti, float A,
-                                          const float (&Bv)[kLPT], float& pA, float (&pB)[kLPT], float& aggA,
-                                          float& aggB, unsigned long long* lane_slots, size_t tile_stride) {
-  L.A[q.tg][q.l4] = A;
+template <class G, bool DYN>
+__device__ __forceinline__ void tile_scan(ChainLds<G>& L, const ThreadPos& q, const TileInfo& ti, const Tags& tg,
+                                          float A, const float (&Bv)[G::LPT], float& pA, float (&pB)[G::LPT],
+                                          float& aggA, float& aggB, unsigned long long* lane_slots,
+                                          size_t tile_stride) {
+  constexpr int LPT = G::LPT;
+  L.A[q.tg][q.lt] = A;
 #pragma unroll
-  for (int i = 0; i < kLPT; ++i) L.B[q.tg][q.l4 * kLPT + i] = Bv[i];
+  for (int i = 0; i < LPT; ++i) L.B[q.tg][q.lt * LPT + i] = Bv[i];
   __syncthreads();
   pA = 1.0f;
 #pragma unroll
-  for (int i = 0; i < kLPT; ++i) pB[i] = 0.0f;
+  for (int i = 0; i < LPT; ++i) pB[i] = 0.0f;
   for (int g = 0; g < q.tg; ++g) {
-    const float a = L.A[g][q.l4];
+    const float a = L.A[g][q.lt];
 #pragma unroll
-    for (int i = 0; i < kLPT; ++i) pB[i] = __builtin_fmaf(a, pB[i], L.B[g][q.l4 * kLPT + i]);
+    for (int i = 0; i < LPT; ++i) pB[i] = __builtin_fmaf(a, pB[i], L.B[g][q.lt * LPT + i]);
     pA *= a;
   }
   aggA = 1.0f;
   aggB = 0.0f;
   if (q.wave == 0) {
-    for (int g = 0; g < kNTG; ++g) {
-      const float a = L.A[g][q.wl >> 2];
+    for (int g = 0; g < G::NTG; ++g) {
+      const float a = L.A[g][q.wl / LPT];
       aggB = __builtin_fmaf(a, aggB, L.B[g][q.wl]);
       aggA *= a;
     }
     if (!ti.is_ckpt && !ti.is_last) {
       unsigned long long* mine = lane_slots + (size_t)ti.tile * tile_stride;
-      if (DYN) publish(mine + 1, ti.tag_agg, aggA);
-      publish(mine, ti.tag_agg, aggB);
+      if (DYN) publish(mine + 1, tg.agg, aggA);
+      publish(mine, tg.agg, aggB);
     }
   }
 }
 
-// Look-back: leaves the carry-in of every lane of the tile in L.carry.
-// `lam_static` is the static lambda of lane wl (unused when DYN).
-template <bool DYN, int R>
-__device__ __forceinline__ void look_back(ChainLds& L, const ThreadPos& q, const TileInfo& ti, float aggA,
-                                          float aggB, const unsigned long long* lane_slots, size_t tile_stride,
-                                          float init_wl, float lam_static_wl, unsigned* hdr_words) {
+// Look-back in two halves so that a caller can issue other loads in between:
+// look_back_issue reads (without waiting) the words this thread needs;
+// look_back_finish waits for the ones not yet published, combines, and
+// leaves the carry-in of every lane in L.carry.  Thread (wave, wl) reads
+// lane wl of WPT predecessor tiles; wave 0 also reads the checkpoint.
+template <class G, bool DYN>
+struct LookBack {
+  unsigned long long vB[G::WPT];
+  unsigned long long vA[DYN ? G::WPT : 1];
+  unsigned long long vck;
+  int beg, end, g0;
+};
+
+template <class G, bool DYN>
+__device__ __forceinline__ void look_back_issue(LookBack<G, DYN>& st, const ThreadPos& q, const TileInfo& ti,
+                                                const unsigned long long* lane_slots, size_t tile_stride) {
+  st.g0 = (ti.tile / kCkpt) * kCkpt;
+  st.beg = st.g0 + q.wave * G::WPT;
+  st.end = min(st.beg + G::WPT, ti.tile);
+#pragma unroll
+  for (int i = 0; i < G::WPT; ++i) {
+    if (st.beg + i < st.end) {
+      const unsigned long long* s = lane_slots + (size_t)(st.beg + i) * tile_stride;
+      st.vB[i] = peek(s);
+      if constexpr (DYN) st.vA[i] = peek(s + 1);
+    }
+  }
+  st.vck = 0;
+  if (q.wave == 0 && st.g0 > 0) st.vck = peek(lane_slots + (size_t)(st.g0 - 1) * tile_stride);
+}
+
+// `lam_static_wl` is the static lambda of lane wl (unused when DYN).
+template <class G, bool DYN>
+__device__ __forceinline__ void look_back_finish(LookBack<G, DYN>& st, ChainLds<G>& L, const ThreadPos& q,
+                                                 const TileInfo& ti, const Tags& tg, float aggA, float aggB,
+                                                 const unsigned long long* lane_slots, size_t tile_stride,
+                                                 float init_wl, float lam_static_wl, unsigned* hdr_words) {
   if (ti.tile > 0) {
-    const int g0 = (ti.tile / kCkpt) * kCkpt;
-    const int beg = g0 + q.wave * kWPT;
-    const int end = min(beg + kWPT, ti.tile);
     float mA = 1.0f, mB = 0.0f;
-    if (beg < end) {
-      const float Afull = DYN ? 1.0f : static_tile_A<R>(lam_static_wl);
-      unsigned long long vB[kWPT];
-      unsigned long long vA[DYN ? kWPT : 1];
+    if (st.beg < st.end) {
+      const float Afull = DYN ? 1.0f : static_tile_A<G>(lam_static_wl);
 #pragma unroll
-      for (int i = 0; i < kWPT; ++i) {
-        if (beg + i < end) {
-          const unsigned long long* s = lane_slots + (size_t)(beg + i) * tile_stride;
-          vB[i] = peek(s);
-          if constexpr (DYN) vA[i] = peek(s + 1);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < kWPT; ++i) {
-        if (beg + i < end) {
-          const unsigned long long* s = lane_slots + (size_t)(beg + i) * tile_stride;
-          const float Bp = await_word(s, vB[i], ti.tag_agg, hdr_words);
+      for (int i = 0; i < G::WPT; ++i) {
+        if (st.beg + i < st.end) {
+          const unsigned long long* s = lane_slots + (size_t)(st.beg + i) * tile_stride;
+          const float Bp = await_word(s, st.vB[i], tg.agg, hdr_words);
           float Ap = Afull;
-          if constexpr (DYN) Ap = await_word(s + 1, vA[i], ti.tag_agg, hdr_words);
+          if constexpr (DYN) Ap = await_word(s + 1, st.vA[i], tg.agg, hdr_words);
           mB = __builtin_fmaf(Ap, mB, Bp);
           mA *= Ap;
         }
@@ -166,23 +222,17 @@ __device__ __forceinline__ void look_back(ChainLds& L, const ThreadPos& q, const
     }
     L.mA[q.wave][q.wl] = mA;
     L.mB[q.wave][q.wl] = mB;
-    float ck = 0.0f;
-    if (q.wave == 0) {
-      if (g0 == 0) {
-        ck = init_wl;
-      } else {
-        const unsigned long long* s = lane_slots + (size_t)(g0 - 1) * tile_stride;
-        ck = await_word(s, peek(s), ti.tag_pre, hdr_words);
-      }
-    }
+    float ck = init_wl;
+    if (q.wave == 0 && st.g0 > 0)
+      ck = await_word(lane_slots + (size_t)(st.g0 - 1) * tile_stride, st.vck, tg.pre, hdr_words);
     __syncthreads();
     if (q.wave == 0) {
       float carry = ck;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) carry = __builtin_fmaf(L.mA[w][q.wl], carry, L.mB[w][q.wl]);
+      for (int w = 0; w < G::WAVES; ++w) carry = __builtin_fmaf(L.mA[w][q.wl], carry, L.mB[w][q.wl]);
       L.carry[q.wl] = carry;
       if (ti.is_ckpt && !ti.is_last)
-        publish(const_cast<unsigned long long*>(lane_slots) + (size_t)ti.tile * tile_stride, ti.tag_pre,
+        publish(const_cast<unsigned long long*>(lane_slots) + (size_t)ti.tile * tile_stride, tg.pre,
                 __builtin_fmaf(aggA, carry, aggB));
     }
   } else if (q.wave == 0) {
@@ -191,15 +241,25 @@ __device__ __forceinline__ void look_back(ChainLds& L, const ThreadPos& q, const
   __syncthreads();
 }
 
-// The last block of the launch re-arms the header for the next launch.
+// Counts this block as finished.  The last block of its class resets the
+// class counters; the last class bumps the epoch for the next launch.
 __device__ __forceinline__ void finish_block(unsigned* hdr_words, unsigned epoch) {
   if (threadIdx.x == 0) {
     WsHeader* hdr = reinterpret_cast<WsHeader*>(hdr_words);
-    const unsigned prev = __hip_atomic_fetch_add(&hdr->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == gridDim.x - 1) {
-      __hip_atomic_store(&hdr->ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&hdr->epoch, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned cls = blockIdx.x & 7u;
+    const unsigned cls_size = (gridDim.x - cls + 7u) >> 3;
+    const unsigned prev = __hip_atomic_fetch_add(&hdr->cls[cls].done, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == cls_size - 1u) {
+      __hip_atomic_store(&hdr->cls[cls].ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&hdr->cls[cls].done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned n_cls = gridDim.x < 8u ? gridDim.x : 8u;
+      const unsigned prev_all = __hip_atomic_fetch_add(&hdr->done_all, 1u, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+      if (prev_all == n_cls - 1u) {
+        __hip_atomic_store(&hdr->done_all, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&hdr->epoch, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
 }

@@ -5,47 +5,52 @@
 //   coeffs     [B, H, K, hd]  fp32
 //   g          [B, S, H]      fp32 (optional, any strides)
 //   ema state  [B, D]         fp32
-//
-// Work decomposition shared by the kernels: a lane-block is 64 consecutive
-// lanes of one batch row; a tile is T consecutive tokens of a lane-block.  A
-// thread owns 4 adjacent lanes (one 16-byte fp32 vector or 8-byte bf16
-// vector) and a run of R consecutive tokens; 16 threads cover the 64 lanes of
-// a row, so each wave instruction touches 4 rows x 256 contiguous bytes.
+// Work decomposition: see TileGeo in osm_kernels.h.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "osm_kernels.h"
+
 namespace osm {
 
-constexpr int kWave = 64;
-constexpr int kLPT = 4;                   // lanes per thread
-constexpr int kTPR = 16;                  // threads per 64-lane row segment
-constexpr int kLanes = kLPT * kTPR;       // lanes per lane-block
-constexpr int kTGW = kWave / kTPR;        // token groups per wave
+constexpr int kLanes = 64;                // lanes per lane-block
 constexpr int kCkpt = 64;                 // checkpoint interval of the look-back, in tiles
 constexpr float kTwoLog2e = 2.8853900817779268f;  // 2*log2(e): tanh via exp2
 
-// Workspace header (first 256 bytes of every workspace).
-//   ticket  next tile ticket of the running launch (reset to 0 by the last block)
-//   done    blocks finished in the running launch  (reset to 0 by the last block)
-//   epoch   launch counter; tags every published look-back word
-//   fault   set to 1 if a launch saw an out-of-range ticket or a look-back
-//           wait exceeded kSpinLimit (results of that launch are invalid);
-//           only a zero fill clears it
+// Workspace header (first kHeaderBytes of every workspace).
+//   epoch      launch counter; tags every published look-back word.  Read by
+//              every block at start, bumped by the last block of the launch.
+//   fault      set to 1 if a look-back wait exceeded kSpinLimit (results of
+//              that launch are invalid); only a zero fill clears it.
+//   done_all   classes finished in the running launch (reset by the last one)
+//   cls[c]     per class c = blockIdx % 8 (one XCD under round-robin
+//              dispatch): `ticket` hands out the class's tiles in order,
+//              `done` counts its finished blocks; the last block of the class
+//              resets both.  One 128-byte line per class: no cross-class
+//              contention.
 struct WsHeader {
-  unsigned ticket;
-  unsigned done;
   unsigned epoch;
-  unsigned fault;
-  unsigned pad[60];
+  unsigned reserved0[2];
+  unsigned fault;          // byte offset 12
+  unsigned reserved1[12];
+  unsigned done_all;       // byte offset 64
+  unsigned reserved2[15];
+  struct {
+    unsigned done;
+    unsigned reserved[15];
+    unsigned ticket;       // separate 64-byte half-line from `done`
+    unsigned pad[15];
+  } cls[8];                // byte offsets 128 + 128 c
 };
-static_assert(sizeof(WsHeader) == 256, "header is 256 bytes");
+static_assert(sizeof(WsHeader) <= kHeaderBytes, "header fits");
 
 // Upper bound on polls of one look-back word (each poll is a device-scope
-// load plus a short sleep, so this is many seconds).  It only guarantees that
-// every wave exits even if the header was corrupted by overlapping calls.
-constexpr unsigned kSpinLimit = 1u << 24;
+// load plus a short sleep: about a second in total).  It only guarantees
+// that every wave exits if the dispatch-order assumption of the look-back
+// ever failed or two calls overlapped on one workspace.
+constexpr unsigned kSpinLimit = 1u << 20;
 
 // A look-back word is one 64-bit value: high 32 bits = (epoch << 2) | kind,
 // low 32 bits = an fp32 payload.  Because tag and payload travel in one
@@ -71,14 +76,18 @@ __device__ __forceinline__ void raise_fault(unsigned* hdr_words) {
 }
 
 // Spin until `slot` carries `tag`, starting from an already-loaded value.
-// The producer of every awaited word has a lower tile ticket, so it is
-// resident or finished and publishes without waiting on anyone: the loop
-// ends.  kSpinLimit bounds it anyway (fault flag, payload 0).
+// The producer of every awaited word was dispatched earlier and publishes
+// without waiting on anything later (osm_chain.h), so the loop ends;
+// kSpinLimit bounds it anyway (fault flag, payload 0).
 __device__ __forceinline__ float await_word(const unsigned long long* slot, unsigned long long w, unsigned tag,
                                             unsigned* hdr_words) {
   unsigned polls = 0;
   while ((unsigned)(w >> 32) != tag) {
-    if (++polls > kSpinLimit) {
+    ++polls;
+    // Give up when over the limit or when another wave already gave up.
+    if (polls > kSpinLimit ||
+        ((polls & 1023u) == 0 &&
+         __hip_atomic_load(hdr_words + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)) {
       raise_fault(hdr_words);
       return 0.0f;
     }
@@ -88,28 +97,77 @@ __device__ __forceinline__ float await_word(const unsigned long long* slot, unsi
   return __uint_as_float((unsigned)w);
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
-// 4-lane vector load / store for fp32 and bf16 element types.
-template <typename T>
-struct Lanes4;
+// N-lane streaming load / store (non-temporal: every element is touched once)
+// for fp32 and bf16.  bf16 is widened exactly; stores round to nearest even
+// (v_cvt_pk_bf16_f32 on gfx950).
+template <typename T, int N>
+struct LaneVec;
 
 template <>
-struct Lanes4<float> {
+struct LaneVec<float, 1> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[1]) { v[0] = __builtin_nontemporal_load(p); }
+  static __device__ __forceinline__ void store(float* p, const float (&v)[1]) { __builtin_nontemporal_store(v[0], p); }
+};
+
+template <>
+struct LaneVec<float, 2> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[2]) {
+    const f32x2 q = __builtin_nontemporal_load(reinterpret_cast<const f32x2*>(p));
+    v[0] = q.x;
+    v[1] = q.y;
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&v)[2]) {
+    const f32x2 q = {v[0], v[1]};
+    __builtin_nontemporal_store(q, reinterpret_cast<f32x2*>(p));
+  }
+};
+
+template <>
+struct LaneVec<float, 4> {
   static __device__ __forceinline__ void load(const float* p, float (&v)[4]) {
     const f32x4 q = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
     v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
   }
   static __device__ __forceinline__ void store(float* p, const float (&v)[4]) {
-    f32x4 q = {v[0], v[1], v[2], v[3]};
+    const f32x4 q = {v[0], v[1], v[2], v[3]};
     __builtin_nontemporal_store(q, reinterpret_cast<f32x4*>(p));
   }
 };
 
 template <>
-struct Lanes4<__bf16> {
+struct LaneVec<__bf16, 1> {
+  static __device__ __forceinline__ void load(const __bf16* p, float (&v)[1]) {
+    const unsigned short q = __builtin_nontemporal_load(reinterpret_cast<const unsigned short*>(p));
+    v[0] = __uint_as_float((unsigned)q << 16);
+  }
+  static __device__ __forceinline__ void store(__bf16* p, const float (&v)[1]) {
+    const __bf16 q = (__bf16)v[0];
+    __builtin_nontemporal_store(__builtin_bit_cast(unsigned short, q), reinterpret_cast<unsigned short*>(p));
+  }
+};
+
+template <>
+struct LaneVec<__bf16, 2> {
+  static __device__ __forceinline__ void load(const __bf16* p, float (&v)[2]) {
+    const unsigned q = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p));
+    v[0] = __uint_as_float(q << 16);
+    v[1] = __uint_as_float(q & 0xffff0000u);
+  }
+  static __device__ __forceinline__ void store(__bf16* p, const float (&v)[2]) {
+    const f32x2 f = {v[0], v[1]};
+    const bf16x2 q = __builtin_convertvector(f, bf16x2);
+    __builtin_nontemporal_store(__builtin_bit_cast(unsigned, q), reinterpret_cast<unsigned*>(p));
+  }
+};
+
+template <>
+struct LaneVec<__bf16, 4> {
   static __device__ __forceinline__ void load(const __bf16* p, float (&v)[4]) {
     const u32x2 q = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
     v[0] = __uint_as_float(q.x << 16);
@@ -117,11 +175,108 @@ struct Lanes4<__bf16> {
     v[2] = __uint_as_float(q.y << 16);
     v[3] = __uint_as_float(q.y & 0xffff0000u);
   }
-  // Round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
   static __device__ __forceinline__ void store(__bf16* p, const float (&v)[4]) {
     const f32x4 f = {v[0], v[1], v[2], v[3]};
     const bf16x4 q = __builtin_convertvector(f, bf16x4);
     __builtin_nontemporal_store(__builtin_bit_cast(u32x2, q), reinterpret_cast<u32x2*>(p));
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Buffer-descriptor access (raw buffer loads/stores).  A descriptor holds a
+// 48-bit base and a byte extent; an access at voffset + soffset beyond the
+// extent reads 0 and drops stores.  Kernels rebase descriptors per tile
+// (uniform, in SGPRs), give each thread a fixed VGPR lane offset (kOffOOB for
+// lanes outside the tensor) and step tokens with a uniform SGPR offset, so
+// no per-element 64-bit address arithmetic or bounds branch is needed.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr int kRsrcWord3 = 0x00020000;       // gfx9-family raw buffer format
+constexpr uint32_t kOffOOB = 0x80000000u;    // out of range of every descriptor we build
+constexpr uint32_t kMaxExtent = 0x7fffffffu;
+constexpr int kNT = 2;                       // cache policy: non-temporal streaming
+
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint64_t extent_bytes) {
+  const uint32_t n = extent_bytes > kMaxExtent ? kMaxExtent : (uint32_t)extent_bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, kRsrcWord3);
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T, int N>
+struct BufVec;
+
+template <>
+struct BufVec<float, 1> {
+  static __device__ __forceinline__ void load(Rsrc r, uint32_t vo, uint32_t so, float (&v)[1]) {
+    v[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, kNT));
+  }
+  static __device__ __forceinline__ void store(Rsrc r, uint32_t vo, uint32_t so, const float (&v)[1]) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, vo, so, kNT);
+  }
+};
+
+template <>
+struct BufVec<float, 2> {
+  static __device__ __forceinline__ void load(Rsrc r, uint32_t vo, uint32_t so, float (&v)[2]) {
+    const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, kNT);
+    v[0] = __uint_as_float(q.x);
+    v[1] = __uint_as_float(q.y);
+  }
+  static __device__ __forceinline__ void store(Rsrc r, uint32_t vo, uint32_t so, const float (&v)[2]) {
+    const u32x2 q = {__float_as_uint(v[0]), __float_as_uint(v[1])};
+    __builtin_amdgcn_raw_buffer_store_b64(q, r, vo, so, kNT);
+  }
+};
+
+template <>
+struct BufVec<float, 4> {
+  static __device__ __forceinline__ void load(Rsrc r, uint32_t vo, uint32_t so, float (&v)[4]) {
+    const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, kNT);
+    v[0] = __uint_as_float(q.x); v[1] = __uint_as_float(q.y); v[2] = __uint_as_float(q.z); v[3] = __uint_as_float(q.w);
+  }
+  static __device__ __forceinline__ void store(Rsrc r, uint32_t vo, uint32_t so, const float (&v)[4]) {
+    const u32x4 q = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+    __builtin_amdgcn_raw_buffer_store_b128(q, r, vo, so, kNT);
+  }
+};
+
+template <>
+struct BufVec<__bf16, 1> {
+  static __device__ __forceinline__ void load(Rsrc r, uint32_t vo, uint32_t so, float (&v)[1]) {
+    v[0] = __uint_as_float((unsigned)__builtin_amdgcn_raw_buffer_load_b16(r, vo, so, kNT) << 16);
+  }
+  static __device__ __forceinline__ void store(Rsrc r, uint32_t vo, uint32_t so, const float (&v)[1]) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (__bf16)v[0]), r, vo, so, kNT);
+  }
+};
+
+template <>
+struct BufVec<__bf16, 2> {
+  static __device__ __forceinline__ void load(Rsrc r, uint32_t vo, uint32_t so, float (&v)[2]) {
+    const unsigned q = __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, kNT);
+    v[0] = __uint_as_float(q << 16);
+    v[1] = __uint_as_float(q & 0xffff0000u);
+  }
+  static __device__ __forceinline__ void store(Rsrc r, uint32_t vo, uint32_t so, const float (&v)[2]) {
+    const f32x2 f = {v[0], v[1]};
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, __builtin_convertvector(f, bf16x2)), r, vo,
+                                          so, kNT);
+  }
+};
+
+template <>
+struct BufVec<__bf16, 4> {
+  static __device__ __forceinline__ void load(Rsrc r, uint32_t vo, uint32_t so, float (&v)[4]) {
+    const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, kNT);
+    v[0] = __uint_as_float(q.x << 16);
+    v[1] = __uint_as_float(q.x & 0xffff0000u);
+    v[2] = __uint_as_float(q.y << 16);
+    v[3] = __uint_as_float(q.y & 0xffff0000u);
+  }
+  static __device__ __forceinline__ void store(Rsrc r, uint32_t vo, uint32_t so, const float (&v)[4]) {
+    const f32x4 f = {v[0], v[1], v[2], v[3]};
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, __builtin_convertvector(f, bf16x4)), r, vo, so,
+                                          kNT);
   }
 };
 

@@ -1,5 +1,5 @@
-// Launch parameters and launcher declarations shared by the kernel files and
-// the C-ABI layer.  Host-visible only; no torch types.
+// Launch parameters, tile geometry and launcher declarations shared by the
+// kernel files and the C-ABI layer.  No torch types.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -8,16 +8,34 @@
 
 namespace osm {
 
-// Tile geometry of the fused kernels: 4 waves of 64 threads, 16 token groups
-// of R tokens each, 64 lanes per lane-block.  The forward uses R = kRun
-// (kTile = 256 tokens); the TTT kernel keeps more per-token state in
-// registers and uses R = kRunTTT (kTileTTT = 128 tokens).
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
-constexpr int kRun = 16;
-constexpr int kTile = kWaves * 4 * kRun;        // 256 tokens
-constexpr int kRunTTT = 8;
-constexpr int kTileTTT = kWaves * 4 * kRunTTT;  // 128 tokens
+// Tile geometry.  A lane-block is 64 consecutive lanes of one batch row; a
+// tile is TILE consecutive tokens of a lane-block and is one workgroup.  A
+// thread owns LPT adjacent lanes and a run of R consecutive tokens; TPR
+// threads cover the 64 lanes of a row, so one wave instruction reads or
+// writes TGW rows x 256 contiguous bytes (fp32).  Token groups (runs) are
+// ordered wave-major: tg = wave * TGW + lane_in_wave / TPR.
+template <int LPT_, int WAVES_, int R_>
+struct TileGeo {
+  static constexpr int LPT = LPT_;            // lanes per thread
+  static constexpr int WAVES = WAVES_;        // waves per workgroup
+  static constexpr int R = R_;                // tokens per thread run
+  static constexpr int THREADS = WAVES * 64;
+  static constexpr int TPR = 64 / LPT;        // threads per 64-lane row
+  static constexpr int TGW = 64 / TPR;        // token groups per wave
+  static constexpr int NTG = WAVES * TGW;     // token groups per tile
+  static constexpr int TILE = NTG * R;        // tokens per tile
+  static constexpr int WPT = 64 / WAVES;      // look-back words per thread (64-tile groups)
+  static_assert(64 % LPT == 0 && 64 % WAVES == 0, "geometry");
+};
+
+// Forward: 2 lanes x 16 tokens per thread, 8 waves -> 256-token tiles.
+using FwdGeo = TileGeo<2, 8, 16>;
+// TTT: keeps x, r and dL/ds per token in registers -> shorter runs.
+using TttGeo = TileGeo<2, 8, 8>;
+
+// Workspace: a kHeaderBytes header (launch epoch, fault word, completion
+// counters), then the look-back words, then (TTT only) per-tile partials.
+constexpr size_t kHeaderBytes = 2048;
 
 struct FwdParams {
   const void* x;
@@ -37,7 +55,8 @@ struct FwdParams {
   int B, S, H, hd, K, D;
   int n_lbd;                   // lane-blocks per batch row = ceil(D / 64)
   int n_lb;                    // B * n_lbd
-  int n_tiles;                 // ceil(S / kTile)
+  int n_lb_pad;                // n_lb rounded up to a multiple of 8; grid = n_lb_pad * n_tiles
+  int n_tiles;                 // ceil(S / TILE)
   float lam_shift, lam_min, lam_max;
   int clamp_out;
   float ttt_scale;             // 2 / (B*(S-1)*D)

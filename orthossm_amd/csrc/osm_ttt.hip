@@ -23,6 +23,7 @@
 namespace osm {
 namespace {
 
+using G = TttGeo;
 constexpr int kChunk = 16;  // tiles merged per thread by the first merge kernel
 
 template <int KP>
@@ -30,68 +31,73 @@ __host__ __device__ constexpr int n_fields() {
   return 2 * KP + 2;  // P_0..P_{KP-1}, Q_0..Q_{KP-1}, Ar, Br
 }
 
+// Sum over the token groups of a wave (lanes wl, wl^TPR, ...).
 __device__ __forceinline__ float wave_sum_tg(float v) {
-  // Sum over the 4 token groups of a wave: lanes wl, wl^16, wl^32, wl^48.
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
+#pragma unroll
+  for (int m = G::TPR; m < 64; m *= 2) v += __shfl_xor(v, m);
   return v;
 }
 
 template <bool DYN, typename XT, typename OT, int KP>
-__global__ void __launch_bounds__(kThreads) cheby_ema_ttt_kernel(const FwdParams p) {
-  constexpr int R = kRunTTT;
+__global__ void __launch_bounds__(G::THREADS) cheby_ema_ttt_kernel(const FwdParams p) {
+  constexpr int R = G::R;
+  constexpr int LPT = G::LPT;
+  constexpr int NTG = G::NTG;
   constexpr int WORDS = DYN ? 2 : 1;
   constexpr int F = n_fields<KP>();
-  __shared__ ChainLds L;
-  __shared__ float sh_y0[kNTG][kLanes];     // target y at each token group's first token
-  __shared__ float sh_rA[kNTG][kTPR];       // reverse map of each run
-  __shared__ float sh_rB[kNTG][kLanes];
-  __shared__ float sh_red[kWaves][2 * KP][kLanes];
+  __shared__ ChainLds<G> L;
+  __shared__ float sh_y0[NTG][kLanes];      // target y at each token group's first token
+  __shared__ float sh_rA[NTG][G::TPR];      // reverse map of each run
+  __shared__ float sh_rB[NTG][kLanes];
+  __shared__ float sh_red[G::WAVES][2 * KP][kLanes];
 
-  const ThreadPos q = thread_pos();
-  const TileInfo ti = claim_tile(L, p.hdr, p.n_lb, p.n_lbd, p.n_tiles);
-  if (!ti.valid) {  // corrupted header: touch nothing, let the launch drain
-    finish_block(p.hdr, ti.epoch);
+  const ThreadPos q = thread_pos<G>();
+  const Tags tags = launch_tags(p.hdr);
+  const TileInfo ti = tile_info(blockIdx.x, p.n_lb, p.n_lb_pad, p.n_lbd, p.n_tiles);
+  if (ti.pad) {
+    finish_block(p.hdr, tags.epoch);
     return;
   }
   const int b = ti.b;
-  const int d0 = ti.lbd * kLanes + q.l4 * kLPT;
+  const int d0 = ti.lbd * kLanes + q.lt * LPT;
   const bool lane_ok = d0 < p.D;
   const int h = lane_ok ? d0 / p.hd : 0;
   const int j0 = d0 - h * p.hd;
-  const int t0 = ti.tile * kTileTTT + q.tg * R;
+  const int t0 = ti.tile * G::TILE + q.tg * R;
   const bool soft_target = p.ttt_target == 1;
 
   const float delta = p.damping[h];
-  float c[kLPT][KP];
+  float c[LPT][KP];
   {
     const float kap = kTwoLog2e * delta;
     const float* cb = p.coeffs + (int64_t)b * p.c_sb + (int64_t)h * p.c_sh + j0;
 #pragma unroll
     for (int k = 0; k < KP; ++k) {
 #pragma unroll
-      for (int i = 0; i < kLPT; ++i)
+      for (int i = 0; i < LPT; ++i)
         c[i][k] = (lane_ok && k < p.K) ? kap * cb[(int64_t)k * p.c_sk + i] : 0.0f;
     }
   }
   const float lam_h = p.lam[h];
 
   const XT* xrow = reinterpret_cast<const XT*>(p.x) + (int64_t)b * p.x_sb + d0;
-  float xv[R][kLPT];
+  float xv[R][LPT];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int t = t0 + r;
     if (lane_ok && t < p.S) {
-      Lanes4<XT>::load(xrow + (int64_t)t * p.x_ss, xv[r]);
+      LaneVec<XT, LPT>::load(xrow + (int64_t)t * p.x_ss, xv[r]);
     } else {
 #pragma unroll
-      for (int i = 0; i < kLPT; ++i) xv[r][i] = 0.0f;
+      for (int i = 0; i < LPT; ++i) xv[r][i] = 0.0f;
     }
   }
   // Target of the token after the run: the next token group's first token
   // (through LDS) or, for the last group, the next tile's first row.
-  float y_after[kLPT] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (q.tg == kNTG - 1 && lane_ok && t0 + R < p.S) Lanes4<XT>::load(xrow + (int64_t)(t0 + R) * p.x_ss, y_after);
+  float y_after[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) y_after[i] = 0.0f;
+  if (q.tg == NTG - 1 && lane_ok && t0 + R < p.S) LaneVec<XT, LPT>::load(xrow + (int64_t)(t0 + R) * p.x_ss, y_after);
 
   float lamv[R];
   {
@@ -110,16 +116,18 @@ __global__ void __launch_bounds__(kThreads) cheby_ema_ttt_kernel(const FwdParams
   }
 
   // Pass 1: r = 1/(1+exp(2 damping p)) per element and the run aggregate.
-  float rr[R][kLPT];
+  float rr[R][LPT];
   float A = 1.0f;
-  float Bv[kLPT] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float Bv[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) Bv[i] = 0.0f;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const float lam = lamv[r];
     const float one_m = 1.0f - lam;
     const float n2 = -2.0f * one_m;
 #pragma unroll
-    for (int i = 0; i < kLPT; ++i) {
+    for (int i = 0; i < LPT; ++i) {
       const float x = xv[r][i];
       rr[r][i] = tanh_r(clenshaw<KP>(softsign(x), c[i]));
       const float w = (x == x) ? __builtin_fmaf(n2, rr[r][i], one_m) : 0.0f;
@@ -130,36 +138,40 @@ __global__ void __launch_bounds__(kThreads) cheby_ema_ttt_kernel(const FwdParams
 
   // Targets at the first token of each run, for the neighbouring run.
 #pragma unroll
-  for (int i = 0; i < kLPT; ++i) {
+  for (int i = 0; i < LPT; ++i) {
     const float x = xv[0][i];
-    sh_y0[q.tg][q.l4 * kLPT + i] = (soft_target && x == x) ? softsign(x) : x;
+    sh_y0[q.tg][q.lt * LPT + i] = (soft_target && x == x) ? softsign(x) : x;
   }
 
   unsigned long long* lane_slots = p.slots + ((size_t)ti.lb * p.n_tiles * kLanes + q.wl) * WORDS;
   const size_t tile_stride = (size_t)kLanes * WORDS;
-  float pA, pB[kLPT], aggA, aggB;
-  tile_scan<DYN>(L, q, ti, A, Bv, pA, pB, aggA, aggB, lane_slots, tile_stride);  // syncs sh_y0 too
+  float pA, pB[LPT], aggA, aggB;
+  tile_scan<G, DYN>(L, q, ti, tags, A, Bv, pA, pB, aggA, aggB, lane_slots, tile_stride);  // syncs sh_y0 too
 
   const int dl = ti.lbd * kLanes + q.wl;
   const bool dl_ok = dl < p.D;
   const float init_wl = (p.ema_init && dl_ok) ? p.ema_init[(int64_t)b * p.D + dl] : 0.0f;
   const float lam_wl = DYN ? 0.0f : p.lam[dl_ok ? dl / p.hd : 0];
-  look_back<DYN, R>(L, q, ti, aggA, aggB, lane_slots, tile_stride, init_wl, lam_wl, p.hdr);
+  {
+    LookBack<G, DYN> lbk;
+    look_back_issue<G, DYN>(lbk, q, ti, lane_slots, tile_stride);
+    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, lane_slots, tile_stride, init_wl, lam_wl, p.hdr);
+  }
 
-  if (q.tg < kNTG - 1) {
+  if (q.tg < NTG - 1) {
 #pragma unroll
-    for (int i = 0; i < kLPT; ++i) y_after[i] = sh_y0[q.tg + 1][q.l4 * kLPT + i];
+    for (int i = 0; i < LPT; ++i) y_after[i] = sh_y0[q.tg + 1][q.lt * LPT + i];
   } else if (soft_target) {
 #pragma unroll
-    for (int i = 0; i < kLPT; ++i) y_after[i] = (y_after[i] == y_after[i]) ? softsign(y_after[i]) : y_after[i];
+    for (int i = 0; i < LPT; ++i) y_after[i] = (y_after[i] == y_after[i]) ? softsign(y_after[i]) : y_after[i];
   }
 
   // Pass 2 (forward): s from the carry, out, and the loss gradient gL.
-  float gl[R][kLPT];
+  float gl[R][LPT];
   {
-    float s[kLPT];
+    float s[LPT];
 #pragma unroll
-    for (int i = 0; i < kLPT; ++i) s[i] = __builtin_fmaf(pA, L.carry[q.l4 * kLPT + i], pB[i]);
+    for (int i = 0; i < LPT; ++i) s[i] = __builtin_fmaf(pA, L.carry[q.lt * LPT + i], pB[i]);
     OT* orow = reinterpret_cast<OT*>(p.out) + (int64_t)b * p.o_sb + d0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -167,9 +179,9 @@ __global__ void __launch_bounds__(kThreads) cheby_ema_ttt_kernel(const FwdParams
       const float lam = lamv[r];
       const float one_m = 1.0f - lam;
       const float n2 = -2.0f * one_m;
-      float o[kLPT];
+      float o[LPT];
 #pragma unroll
-      for (int i = 0; i < kLPT; ++i) {
+      for (int i = 0; i < LPT; ++i) {
         const float x = xv[r][i];
         const float w = (x == x && t < p.S) ? __builtin_fmaf(n2, rr[r][i], one_m) : 0.0f;
         s[i] = __builtin_fmaf(lam, s[i], w);
@@ -184,21 +196,23 @@ __global__ void __launch_bounds__(kThreads) cheby_ema_ttt_kernel(const FwdParams
         const bool pass = !p.clamp_out || (s[i] >= -1.0f && s[i] <= 1.0f);
         gl[r][i] = (t < p.S - 1 && pass) ? p.ttt_scale * (o[i] - y) : 0.0f;
       }
-      if (lane_ok && t < p.S) Lanes4<OT>::store(orow + (int64_t)t * p.o_ss, o);
+      if (lane_ok && t < p.S) LaneVec<OT, LPT>::store(orow + (int64_t)t * p.o_ss, o);
     }
-    if (ti.is_last && q.tg == kNTG - 1 && lane_ok && p.ema_final) {
+    if (ti.is_last && q.tg == NTG - 1 && lane_ok && p.ema_final) {
 #pragma unroll
-      for (int i = 0; i < kLPT; ++i) p.ema_final[(int64_t)b * p.D + d0 + i] = s[i];
+      for (int i = 0; i < LPT; ++i) p.ema_final[(int64_t)b * p.D + d0 + i] = s[i];
     }
   }
 
   // Reverse sweep over the run: at (local adjoint), Lam (decay to run end).
-  float P[KP][kLPT], Q[KP][kLPT];
+  float P[KP][LPT], Q[KP][LPT];
 #pragma unroll
   for (int k = 0; k < KP; ++k)
 #pragma unroll
-    for (int i = 0; i < kLPT; ++i) P[k][i] = Q[k][i] = 0.0f;
-  float at[kLPT] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < LPT; ++i) P[k][i] = Q[k][i] = 0.0f;
+  float at[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) at[i] = 0.0f;
   float Lam = 1.0f, lam_next = 1.0f;
   const float dsc = 4.0f * delta;  // 1 - z^2 = 4 r (1 - r)
 #pragma unroll
@@ -208,7 +222,7 @@ __global__ void __launch_bounds__(kThreads) cheby_ema_ttt_kernel(const FwdParams
     Lam *= lam_next;
     const float dl_scale = (t < p.S) ? (1.0f - lam) * dsc : 0.0f;
 #pragma unroll
-    for (int i = 0; i < kLPT; ++i) {
+    for (int i = 0; i < LPT; ++i) {
       const float x = xv[r][i];
       const bool ok = x == x;
       at[i] = __builtin_fmaf(lam_next, at[i], gl[r][i]);
@@ -238,53 +252,55 @@ __global__ void __launch_bounds__(kThreads) cheby_ema_ttt_kernel(const FwdParams
   }
   // Run reverse map: rho_prev = lam[t0] * (at[t0] + Lam[t0] * rho_run).
   const float rA = lam_next * Lam;
-  float rB[kLPT];
+  float rB[LPT];
 #pragma unroll
-  for (int i = 0; i < kLPT; ++i) rB[i] = lam_next * at[i];
-  sh_rA[q.tg][q.l4] = rA;
+  for (int i = 0; i < LPT; ++i) rB[i] = lam_next * at[i];
+  sh_rA[q.tg][q.lt] = rA;
 #pragma unroll
-  for (int i = 0; i < kLPT; ++i) sh_rB[q.tg][q.l4 * kLPT + i] = rB[i];
+  for (int i = 0; i < LPT; ++i) sh_rB[q.tg][q.lt * LPT + i] = rB[i];
   __syncthreads();
 
   // rho_run(tg) = alpha + beta * rho_tile, from the later runs in fixed order.
-  float alpha[kLPT] = {0.0f, 0.0f, 0.0f, 0.0f};
-  float beta = 1.0f;
-  for (int g = kNTG - 1; g > q.tg; --g) {
-    const float a = sh_rA[g][q.l4];
+  float alpha[LPT];
 #pragma unroll
-    for (int i = 0; i < kLPT; ++i) alpha[i] = __builtin_fmaf(a, alpha[i], sh_rB[g][q.l4 * kLPT + i]);
+  for (int i = 0; i < LPT; ++i) alpha[i] = 0.0f;
+  float beta = 1.0f;
+  for (int g = NTG - 1; g > q.tg; --g) {
+    const float a = sh_rA[g][q.lt];
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) alpha[i] = __builtin_fmaf(a, alpha[i], sh_rB[g][q.lt * LPT + i]);
     beta *= a;
   }
   float* part = p.partials + ((size_t)ti.lb * p.n_tiles + ti.tile) * F * kLanes;
   if (q.tg == 0) {
     // Tile reverse map: rho_prev_tile = rA*(alpha + beta*rho_tile) + rB.
 #pragma unroll
-    for (int i = 0; i < kLPT; ++i) {
-      part[(size_t)(2 * KP) * kLanes + q.l4 * kLPT + i] = rA * beta;
-      part[(size_t)(2 * KP + 1) * kLanes + q.l4 * kLPT + i] = __builtin_fmaf(rA, alpha[i], rB[i]);
+    for (int i = 0; i < LPT; ++i) {
+      part[(size_t)(2 * KP) * kLanes + q.lt * LPT + i] = rA * beta;
+      part[(size_t)(2 * KP + 1) * kLanes + q.lt * LPT + i] = __builtin_fmaf(rA, alpha[i], rB[i]);
     }
   }
   // Tile partials: P' = sum_runs (P + alpha Q), Q' = sum_runs beta Q.
 #pragma unroll
   for (int k = 0; k < KP; ++k) {
 #pragma unroll
-    for (int i = 0; i < kLPT; ++i) {
+    for (int i = 0; i < LPT; ++i) {
       const float pv = wave_sum_tg(__builtin_fmaf(alpha[i], Q[k][i], P[k][i]));
       const float qv = wave_sum_tg(beta * Q[k][i]);
-      if ((q.wl >> 4) == 0) {
-        sh_red[q.wave][k][q.l4 * kLPT + i] = pv;
-        sh_red[q.wave][KP + k][q.l4 * kLPT + i] = qv;
+      if (q.wl < G::TPR) {
+        sh_red[q.wave][k][q.lt * LPT + i] = pv;
+        sh_red[q.wave][KP + k][q.lt * LPT + i] = qv;
       }
     }
   }
   __syncthreads();
-  for (int v = q.wave; v < 2 * KP; v += kWaves) {
+  for (int v = q.wave; v < 2 * KP; v += G::WAVES) {
     float acc = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) acc += sh_red[w][v][q.wl];
+    for (int w = 0; w < G::WAVES; ++w) acc += sh_red[w][v][q.wl];
     part[(size_t)v * kLanes + q.wl] = acc;
   }
-  finish_block(p.hdr, ti.epoch);
+  finish_block(p.hdr, tags.epoch);
 }
 
 // Merge formula, earlier tile/chunk e followed by combined later part c:
@@ -349,8 +365,8 @@ __global__ void __launch_bounds__(64) ttt_finalize(const float* chunks, float* g
 
 template <bool DYN, typename XT, typename OT, int KP>
 hipError_t launch_all(const FwdParams& p, float* grad, hipStream_t stream) {
-  const unsigned grid = (unsigned)p.n_lb * (unsigned)p.n_tiles;
-  hipLaunchKernelGGL((cheby_ema_ttt_kernel<DYN, XT, OT, KP>), dim3(grid), dim3(kThreads), 0, stream, p);
+  const unsigned grid = (unsigned)p.n_lb_pad * (unsigned)p.n_tiles;
+  hipLaunchKernelGGL((cheby_ema_ttt_kernel<DYN, XT, OT, KP>), dim3(grid), dim3(G::THREADS), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int n_chunks = (p.n_tiles + kChunk - 1) / kChunk;

@@ -67,10 +67,10 @@ def _args(**kw):
 def test_workspace_bytes_formula():
     lib = nat.load()
     a = _args()
-    # 256-byte header + one 8-byte word per (lane-block, 256-token tile, lane)
-    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 256 + 32 * 64 * 64 * 8
+    # 2048-byte header + one 8-byte word per (lane-block, 256-token tile, lane)
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 64 * 64 * 8
     a.g = 0x10000
-    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 256 + 32 * 64 * 64 * 16
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 64 * 64 * 16
     a.K = 9
     assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 0
 
