@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -78,7 +79,8 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
       return fail(OSM_E_LAYOUT, "out rows/batches overlap (out_stride_s=%lld < D or out_stride_b too small)",
                   (long long)a->out_stride_s);
     // One tile's byte span must fit a buffer descriptor's 31-bit offsets.
-    const int64_t tile_rows = osm::FwdGeo::TILE > osm::TttGeo::TILE ? osm::FwdGeo::TILE : osm::TttGeo::TILE;
+    const int64_t tile_rows = std::max<int64_t>(std::max(osm::FwdGeoT<true>::TILE, osm::FwdGeoT<false>::TILE),
+                                                osm::TttGeo::TILE);
     if ((tile_rows * a->x_stride_s + D) * xs >= (int64_t(1) << 31) ||
         (tile_rows * a->out_stride_s + D) * os >= (int64_t(1) << 31))
       return fail(OSM_E_LAYOUT, "token stride too large for 31-bit tile offsets");
@@ -93,7 +95,7 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
       return fail(OSM_E_LAYOUT, "coeffs strides must be non-negative and fit 31-bit offsets");
   }
   const int64_t n_lbd = (D + 63) / 64;
-  const int64_t tile = ttt ? osm::TttGeo::TILE : osm::FwdGeo::TILE;
+  const int64_t tile = ttt ? osm::TttGeo::TILE : (geo->dyn ? osm::FwdGeoT<true>::TILE : osm::FwdGeoT<false>::TILE);
   const int64_t n_tiles = (a->S + tile - 1) / tile;
   const int64_t n_lb = a->B * n_lbd;
   const int64_t n_lb_pad = (n_lb + 7) / 8 * 8;

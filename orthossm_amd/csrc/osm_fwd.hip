@@ -8,7 +8,7 @@
 // over persistent workgroups and chained by the single-pass look-back of
 // osm_chain.h.
 //
-// Each workgroup (FwdGeo: 512 threads) loops over tiles of its class, with
+// Each workgroup (FwdGeoT: 512 threads) loops over tiles of its class, with
 // the next tile's x, g and coefficients loaded while the current tile is
 // processed:
 //   1. pass 1 on the prefetched tile: w = (1-lam) * tanh(damping * p(u)) in
@@ -31,7 +31,8 @@
 namespace osm {
 namespace {
 
-using G = FwdGeo;
+template <bool DYN>
+using Geo = FwdGeoT<DYN>;
 
 // Fast path: w = (1 - lam) * tanh(damping * p) with c pre-scaled by
 // 2*log2(e)*damping.  softsign as copysign(1 - 1/(1 + |x|), x): +-Inf and
@@ -65,13 +66,13 @@ template <bool DYN, typename XT, typename OT>
 __device__ __forceinline__ TileAddr<DYN, XT, OT> tile_addr(const FwdParams& p, const ThreadPos& q,
                                                            const TileInfo& ti) {
   TileAddr<DYN, XT, OT> a;
-  const int t_tile = ti.tile * G::TILE;
-  const int d0 = ti.lbd * kLanes + q.lt * G::LPT;
+  const int t_tile = ti.tile * Geo<DYN>::TILE;
+  const int d0 = ti.lbd * kLanes + q.lt * Geo<DYN>::LPT;
   const bool lane_ok = d0 < p.D;
   const uint64_t rows_after = (uint64_t)(p.S - 1 - t_tile);
   a.h = lane_ok ? d0 / p.hd : 0;
   const int j0 = d0 - a.h * p.hd;
-  const int64_t row0 = (int64_t)q.tg * G::R;
+  const int64_t row0 = (int64_t)q.tg * Geo<DYN>::R;
   // x and out: the extent ends after row S-1, so padding rows read 0 and
   // their stores are dropped.
   const char* xb = static_cast<const char*>(p.x) + ((int64_t)ti.b * p.x_sb + (int64_t)t_tile * p.x_ss) * sizeof(XT);
@@ -98,9 +99,9 @@ __device__ __forceinline__ TileAddr<DYN, XT, OT> tile_addr(const FwdParams& p, c
 // Registers holding one tile's inputs for this thread.
 template <bool DYN, int KP>
 struct TileInputs {
-  float x[G::R][G::LPT];
-  float g[DYN ? G::R : 1];
-  float c[G::LPT][KP];   // raw coefficients (0 beyond K and for lanes >= D)
+  float x[Geo<DYN>::R][Geo<DYN>::LPT];
+  float g[DYN ? Geo<DYN>::R : 1];
+  float c[Geo<DYN>::LPT][KP];   // raw coefficients (0 beyond K and for lanes >= D)
   float lam, damp;
 };
 
@@ -118,14 +119,14 @@ __device__ __forceinline__ void load_tile(TileInputs<DYN, KP>& in, const FwdPara
                                           const TileAddr<DYN, XT, OT>& a) {
   uint32_t so = 0;
 #pragma unroll
-  for (int r = 0; r < G::R; ++r) {
-    BufVec<XT, G::LPT>::load(a.x, a.vx, so, in.x[r]);
+  for (int r = 0; r < Geo<DYN>::R; ++r) {
+    BufVec<XT, Geo<DYN>::LPT>::load(a.x, a.vx, so, in.x[r]);
     so = next_off(so, a.sx);
   }
   if constexpr (DYN) {
     uint32_t sg = 0;
 #pragma unroll
-    for (int r = 0; r < G::R; ++r) {
+    for (int r = 0; r < Geo<DYN>::R; ++r) {
       float gv[1];
       BufVec<float, 1>::load(a.g, a.vg, sg, gv);
       in.g[r] = gv[0];
@@ -135,16 +136,16 @@ __device__ __forceinline__ void load_tile(TileInputs<DYN, KP>& in, const FwdPara
   uint32_t sc = 0;
 #pragma unroll
   for (int k = 0; k < KP; ++k) {
-    float cv[G::LPT];
+    float cv[Geo<DYN>::LPT];
     if (k < p.K) {
-      BufVec<float, G::LPT>::load(a.c, a.vc, sc, cv);
+      BufVec<float, Geo<DYN>::LPT>::load(a.c, a.vc, sc, cv);
       sc = next_off(sc, a.sc);
     } else {
 #pragma unroll
-      for (int i = 0; i < G::LPT; ++i) cv[i] = 0.0f;
+      for (int i = 0; i < Geo<DYN>::LPT; ++i) cv[i] = 0.0f;
     }
 #pragma unroll
-    for (int i = 0; i < G::LPT; ++i) in.c[i][k] = cv[i];
+    for (int i = 0; i < Geo<DYN>::LPT; ++i) in.c[i][k] = cv[i];
   }
   in.lam = p.lam[a.h];
   in.damp = p.damping[a.h];
@@ -155,13 +156,13 @@ __device__ __forceinline__ void load_tile(TileInputs<DYN, KP>& in, const FwdPara
 // they only feed the last tile's own aggregate (never published) and the
 // carries of later, equally padded, token groups, whose stores are dropped.
 template <bool DYN, int KP>
-__device__ __forceinline__ void pass1(TileInputs<DYN, KP>& in, const FwdParams& p, const float (&c)[G::LPT][KP],
-                                      float (&lamv)[DYN ? G::R : 1], float& A, float (&Bv)[G::LPT]) {
+__device__ __forceinline__ void pass1(TileInputs<DYN, KP>& in, const FwdParams& p, const float (&c)[Geo<DYN>::LPT][KP],
+                                      float (&lamv)[DYN ? Geo<DYN>::R : 1], float& A, float (&Bv)[Geo<DYN>::LPT]) {
   A = 1.0f;
 #pragma unroll
-  for (int i = 0; i < G::LPT; ++i) Bv[i] = 0.0f;
+  for (int i = 0; i < Geo<DYN>::LPT; ++i) Bv[i] = 0.0f;
 #pragma unroll
-  for (int r = 0; r < G::R; ++r) {
+  for (int r = 0; r < Geo<DYN>::R; ++r) {
     float lam = in.lam;
     if constexpr (DYN) {
       lam = __builtin_amdgcn_fmed3f(__builtin_fmaf(p.lam_shift, in.g[r], in.lam), p.lam_min, p.lam_max);
@@ -170,7 +171,7 @@ __device__ __forceinline__ void pass1(TileInputs<DYN, KP>& in, const FwdParams& 
     const float one_m = 1.0f - lam;
     const float n2 = -2.0f * one_m;
 #pragma unroll
-    for (int i = 0; i < G::LPT; ++i) {
+    for (int i = 0; i < Geo<DYN>::LPT; ++i) {
       const float w = ema_input_fast<KP>(in.x[r][i], c[i], one_m, n2);
       in.x[r][i] = w;
       Bv[i] = __builtin_fmaf(lam, Bv[i], w);
@@ -184,18 +185,18 @@ __device__ __forceinline__ void pass1(TileInputs<DYN, KP>& in, const FwdParams& 
 // special-value handling.
 template <bool DYN, typename XT, typename OT, int KP>
 __device__ __forceinline__ void pass1_exact(TileInputs<DYN, KP>& in, const FwdParams& p, const TileAddr<DYN, XT, OT>& a,
-                                         const float (&c)[G::LPT][KP], const float (&lamv)[DYN ? G::R : 1],
-                                         float (&Bv)[G::LPT]) {
+                                         const float (&c)[Geo<DYN>::LPT][KP], const float (&lamv)[DYN ? Geo<DYN>::R : 1],
+                                         float (&Bv)[Geo<DYN>::LPT]) {
 #pragma unroll
-  for (int i = 0; i < G::LPT; ++i) Bv[i] = 0.0f;
-  for (int r = 0; r < G::R; ++r) {
-    float xv[G::LPT];
-    BufVec<XT, G::LPT>::load(a.x, a.vx, (uint32_t)r * a.sx, xv);
+  for (int i = 0; i < Geo<DYN>::LPT; ++i) Bv[i] = 0.0f;
+  for (int r = 0; r < Geo<DYN>::R; ++r) {
+    float xv[Geo<DYN>::LPT];
+    BufVec<XT, Geo<DYN>::LPT>::load(a.x, a.vx, (uint32_t)r * a.sx, xv);
     const float lam = DYN ? lamv[r] : in.lam;
     const float one_m = 1.0f - lam;
     const float n2 = -2.0f * one_m;
 #pragma unroll
-    for (int i = 0; i < G::LPT; ++i) {
+    for (int i = 0; i < Geo<DYN>::LPT; ++i) {
       const float w = ema_input_exact<KP>(xv[i], c[i], one_m, n2);
       in.x[r][i] = w;
       Bv[i] = __builtin_fmaf(lam, Bv[i], w);
@@ -206,9 +207,10 @@ __device__ __forceinline__ void pass1_exact(TileInputs<DYN, KP>& in, const FwdPa
 // PERSIST: persistent blocks taking tiles by class tickets, with the next
 // tile prefetched; otherwise one tile per block (v = blockIdx.x).
 template <bool DYN, typename XT, typename OT, int KP, bool PERSIST>
-__global__ void __launch_bounds__(G::THREADS) cheby_ema_fwd_kernel(const FwdParams p) {
-  constexpr int R = G::R;
-  constexpr int LPT = G::LPT;
+__global__ void __launch_bounds__(Geo<DYN>::THREADS) cheby_ema_fwd_kernel(const FwdParams p) {
+  using G = Geo<DYN>;
+  constexpr int R = Geo<DYN>::R;
+  constexpr int LPT = Geo<DYN>::LPT;
   constexpr int WORDS = DYN ? 2 : 1;
   __shared__ ChainLds<G> L;
 
@@ -288,7 +290,7 @@ __global__ void __launch_bounds__(G::THREADS) cheby_ema_fwd_kernel(const FwdPara
     float s[LPT];
 #pragma unroll
     for (int i = 0; i < LPT; ++i) s[i] = __builtin_fmaf(pA, L.carry[q.lt * LPT + i], pB[i]);
-    const int t0 = ti.tile * G::TILE + q.tg * R;
+    const int t0 = ti.tile * Geo<DYN>::TILE + q.tg * R;
     const int r_last = p.S - 1 - t0;   // run index of token S-1 (in range only for one run)
     float s_last[LPT];
     uint32_t so = 0;
@@ -355,13 +357,13 @@ hipError_t launch_one(const FwdParams& p, hipStream_t stream) {
   const int n_virt = p.n_lb_pad * p.n_tiles;
   if (persistent_schedule()) {
     const void* fn = reinterpret_cast<const void*>(&cheby_ema_fwd_kernel<DYN, XT, OT, KP, true>);
-    int grid = resident_blocks(fn, G::THREADS);
+    int grid = resident_blocks(fn, Geo<DYN>::THREADS);
     grid = grid < n_virt ? grid : n_virt;
     grid = grid / 8 * 8;
     if (grid < 8) grid = 8;
-    hipLaunchKernelGGL((cheby_ema_fwd_kernel<DYN, XT, OT, KP, true>), dim3(grid), dim3(G::THREADS), 0, stream, p);
+    hipLaunchKernelGGL((cheby_ema_fwd_kernel<DYN, XT, OT, KP, true>), dim3(grid), dim3(Geo<DYN>::THREADS), 0, stream, p);
   } else {
-    hipLaunchKernelGGL((cheby_ema_fwd_kernel<DYN, XT, OT, KP, false>), dim3(n_virt), dim3(G::THREADS), 0, stream,
+    hipLaunchKernelGGL((cheby_ema_fwd_kernel<DYN, XT, OT, KP, false>), dim3(n_virt), dim3(Geo<DYN>::THREADS), 0, stream,
                        p);
   }
   return hipGetLastError();

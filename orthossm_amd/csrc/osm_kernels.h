@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace osm {
 
 // Tile geometry.  A lane-block is 64 consecutive lanes of one batch row; a
@@ -28,8 +30,12 @@ struct TileGeo {
   static_assert(64 % LPT == 0 && 64 % WAVES == 0, "geometry");
 };
 
-// Forward: 2 lanes x 16 tokens per thread, 8 waves -> 256-token tiles.
-using FwdGeo = TileGeo<2, 8, 16>;
+// Forward: 2 lanes per thread, 8 waves.  Static lambda: 32-token runs
+// (512-token tiles); dynamic lambda keeps a per-token lambda and g in
+// registers, so 16-token runs (256-token tiles).  Chosen by measurement on
+// MI355X at BASELINE configs[1] and configs[3].
+template <bool DYN>
+using FwdGeoT = typename std::conditional<DYN, TileGeo<2, 8, 16>, TileGeo<2, 8, 32>>::type;
 // TTT: keeps x, r and dL/ds per token in registers -> shorter runs.
 using TttGeo = TileGeo<2, 8, 8>;
 
