@@ -32,6 +32,7 @@ int ok() {
 
 struct Geometry {
   int n_lbd = 0, n_lb = 0, n_lb_pad = 0, n_tiles = 0;
+  int tile = 0;        // tokens per tile
   bool dyn = false;
   int kpad = 8;
   bool empty = false;  // B == 0 or S == 0
@@ -40,7 +41,7 @@ struct Geometry {
 bool aligned4(const void* p, int esize) { return ((uintptr_t)p % (uintptr_t)(4 * esize)) == 0; }
 
 // Validates `a` without touching the GPU and fills `geo` for the forward
-// (ttt = false, 256-token tiles) or the TTT kernel (128-token tiles).
+// (ttt = false; tile size from osm::fwd_tile_tokens) or the TTT kernel.
 int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_only = false) {
   if (!a) return fail(OSM_E_ARG, "args is NULL");
   if (a->abi_version != OSM_ABI_VERSION)
@@ -79,8 +80,7 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
       return fail(OSM_E_LAYOUT, "out rows/batches overlap (out_stride_s=%lld < D or out_stride_b too small)",
                   (long long)a->out_stride_s);
     // One tile's byte span must fit a buffer descriptor's 31-bit offsets.
-    const int64_t tile_rows = std::max<int64_t>(std::max(osm::FwdGeoT<true>::TILE, osm::FwdGeoT<false>::TILE),
-                                                osm::TttGeo::TILE);
+    const int64_t tile_rows = std::max<int64_t>(osm::kMaxFwdTile, osm::TttGeo::TILE);
     if ((tile_rows * a->x_stride_s + D) * xs >= (int64_t(1) << 31) ||
         (tile_rows * a->out_stride_s + D) * os >= (int64_t(1) << 31))
       return fail(OSM_E_LAYOUT, "token stride too large for 31-bit tile offsets");
@@ -95,9 +95,9 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
       return fail(OSM_E_LAYOUT, "coeffs strides must be non-negative and fit 31-bit offsets");
   }
   const int64_t n_lbd = (D + 63) / 64;
-  const int64_t tile = ttt ? osm::TttGeo::TILE : (geo->dyn ? osm::FwdGeoT<true>::TILE : osm::FwdGeoT<false>::TILE);
-  const int64_t n_tiles = (a->S + tile - 1) / tile;
   const int64_t n_lb = a->B * n_lbd;
+  const int64_t tile = ttt ? osm::TttGeo::TILE : osm::fwd_tile_tokens(geo->dyn, n_lb, a->S);
+  const int64_t n_tiles = (a->S + tile - 1) / tile;
   const int64_t n_lb_pad = (n_lb + 7) / 8 * 8;
   if (n_lb_pad * n_tiles >= (int64_t(1) << 31) || a->S >= (int64_t(1) << 31) - tile)
     return fail(OSM_E_SHAPE, "problem too large: %lld tiles", (long long)(n_lb * n_tiles));
@@ -105,6 +105,7 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
   geo->n_lb = (int)n_lb;
   geo->n_lb_pad = (int)n_lb_pad;
   geo->n_tiles = (int)n_tiles;
+  geo->tile = (int)tile;
   return OSM_OK;
 }
 
@@ -173,10 +174,10 @@ int hip_fail(hipError_t e, const char* what) {
 // workspace is cleared on the stream first.  A workspace seen for the first
 // time is cleared too, unless osm_workspace_init zeroed it.
 struct Layout {
-  int n_lb, n_tiles, kpad;
+  int n_lb, n_tiles, tile, kpad;
   bool dyn, ttt;
   bool operator==(const Layout& o) const {
-    return n_lb == o.n_lb && n_tiles == o.n_tiles && kpad == o.kpad && dyn == o.dyn && ttt == o.ttt;
+    return n_lb == o.n_lb && n_tiles == o.n_tiles && tile == o.tile && kpad == o.kpad && dyn == o.dyn && ttt == o.ttt;
   }
 };
 const Layout kZeroed{-1, -1, -1, false, false};
@@ -184,7 +185,7 @@ std::mutex g_ws_mu;
 std::unordered_map<uintptr_t, Layout> g_ws_layout;
 
 int prepare_workspace(void* ws, size_t need, const Geometry& geo, bool ttt, hipStream_t stream) {
-  const Layout now{geo.n_lb, geo.n_tiles, geo.kpad, geo.dyn, ttt};
+  const Layout now{geo.n_lb, geo.n_tiles, geo.tile, geo.kpad, geo.dyn, ttt};
   bool clear;
   {
     std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -251,7 +252,7 @@ int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t worksp
   rc = prepare_workspace(workspace, osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn), geo, false, st);
   if (rc != OSM_OK) return rc;
   const osm::FwdParams p = make_params(args, geo, workspace);
-  const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, geo.kpad, st);
+  const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, geo.tile, geo.kpad, st);
   if (e != hipSuccess) return hip_fail(e, "forward kernel launch");
   return ok();
 }

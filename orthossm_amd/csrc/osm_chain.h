@@ -16,18 +16,11 @@
 // v % n_lb_pad, with n_lb_pad = n_lb rounded up to a multiple of 8 (virtual
 // tiles with lane-block >= n_lb are padding and are skipped).  A tile waits
 // only on earlier tiles of its lane-block: v - k*n_lb_pad, the same class
-// v % 8.  Two ways of handing out tiles keep every awaited tile with a
-// producer that already runs:
-//   * persistent (forward kernel): each class has a ticket counter; a block
-//     of class blockIdx % 8 takes tickets of its class one at a time
-//     (ticket_to_tile).  A ticket is taken by a running block, and every
-//     tile a block waits on has a smaller ticket of the same class, so its
-//     producer is running or done: no assumption on dispatch order or
-//     co-residency.
-//   * one tile per block (TTT kernel): block b handles v = b.  Awaited blocks
-//     have a lower index at a stride that is a multiple of 8; workgroups go
-//     to the 8 XCDs round-robin by index and in index order within an XCD,
-//     so each awaited block sits on the same XCD and was dispatched first.
+// v % 8.  Block b handles v = b.  Awaited blocks have a lower index at a
+// stride that is a multiple of 8; workgroups go to the 8 XCDs round-robin by
+// index and in index order within an XCD, so each awaited block sits on the
+// same XCD and was dispatched before the waiter.  The waits are bounded
+// (kSpinLimit), so a broken assumption surfaces as a fault flag, not a hang.
 #pragma once
 
 #include "osm_device.h"
@@ -42,7 +35,6 @@ struct ChainLds {
   float mA[G::WAVES][kLanes];   // look-back partial maps per wave
   float mB[G::WAVES][kLanes];
   float carry[kLanes];          // resolved carry-in of the tile
-  int next_v;                   // broadcast of the next ticket (persistent kernels)
 };
 
 struct TileInfo {
@@ -93,26 +85,6 @@ __device__ __forceinline__ TileInfo tile_info(int v, int n_lb, int n_lb_pad, int
   ti.is_last = ti.tile == n_tiles - 1;
   ti.is_ckpt = (ti.tile % kCkpt) == kCkpt - 1;
   return ti;
-}
-
-__device__ __forceinline__ unsigned take_ticket(unsigned* hdr_words, int cls) {
-  WsHeader* hdr = reinterpret_cast<WsHeader*>(hdr_words);
-  return __hip_atomic_fetch_add(&hdr->cls[cls].ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Lane-blocks of class cls (lb % 8 == cls, lb < n_lb).
-__device__ __forceinline__ int class_lane_blocks(int cls, int n_lb) { return cls < n_lb ? (n_lb - cls + 7) / 8 : 0; }
-
-// Virtual tile v = tile * n_lb_pad + lb of ticket k of class cls: tickets
-// walk the class's lane-blocks fastest, then tiles, so ticket k waits only
-// on tickets k - m, k - 2m, ... (m lane-blocks in the class).  Returns
-// n_virt when the class is exhausted.
-__device__ __forceinline__ int ticket_to_tile(unsigned k, int cls, int n_lb, int n_lb_pad, int n_tiles) {
-  const int m = class_lane_blocks(cls, n_lb);
-  if (m == 0 || (int)k >= m * n_tiles) return n_lb_pad * n_tiles;
-  const int tile = (int)k / m;
-  const int lb = cls + 8 * ((int)k - tile * m);
-  return tile * n_lb_pad + lb;
 }
 
 // Aggregate A of a full tile under a static lambda, in the same
@@ -242,7 +214,7 @@ __device__ __forceinline__ void look_back_finish(LookBack<G, DYN>& st, ChainLds<
 }
 
 // Counts this block as finished.  The last block of its class resets the
-// class counters; the last class bumps the epoch for the next launch.
+// class counter; the last class bumps the epoch for the next launch.
 __device__ __forceinline__ void finish_block(unsigned* hdr_words, unsigned epoch) {
   if (threadIdx.x == 0) {
     WsHeader* hdr = reinterpret_cast<WsHeader*>(hdr_words);
@@ -251,7 +223,6 @@ __device__ __forceinline__ void finish_block(unsigned* hdr_words, unsigned epoch
     const unsigned prev = __hip_atomic_fetch_add(&hdr->cls[cls].done, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
     if (prev == cls_size - 1u) {
-      __hip_atomic_store(&hdr->cls[cls].ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&hdr->cls[cls].done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const unsigned n_cls = gridDim.x < 8u ? gridDim.x : 8u;
       const unsigned prev_all = __hip_atomic_fetch_add(&hdr->done_all, 1u, __ATOMIC_RELAXED,

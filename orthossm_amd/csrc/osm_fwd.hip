@@ -4,75 +4,49 @@
 // Reference counterpart: the forward part of _ortho_megakernel
 // (sdpc_kernel.py:2006-2124) and _fused_clenshaw_ema_kernel
 // (sdpc_kernel.py:988-1209).  The reference walks S serially inside each of
-// B*H*ceil(hd/32) programs; here tiles of 256 tokens x 64 lanes are spread
-// over persistent workgroups and chained by the single-pass look-back of
-// osm_chain.h.
+// B*H*ceil(hd/32) programs; here every (lane-block, tile) is one workgroup
+// and tiles are chained by the single-pass look-back of osm_chain.h.
 //
-// Each workgroup (FwdGeoT: 512 threads) loops over tiles of its class, with
-// the next tile's x, g and coefficients loaded while the current tile is
-// processed:
-//   1. pass 1 on the prefetched tile: w = (1-lam) * tanh(damping * p(u)) in
-//      registers; serial EMA from 0 over each thread's run -> (A, B);
-//   2. token-group scan in LDS -> tile aggregate, published;
-//   3. look-back loads issued, then the next tile's loads issued (vector
-//      memory counters retire in order, so the look-back wait does not wait
-//      for the prefetch);
-//   4. carry-in resolved; replay s = lam*s + w from it, store out.
+// Per workgroup (512 threads; tile of G::TILE tokens x 64 lanes):
+//   1. load x (and g, coefficients) through buffer descriptors;
+//   2. pass 1: w = (1-lam) * tanh(damping * p(u)) in registers, serial EMA
+//      from 0 over each thread's run -> run aggregate (A, B);
+//   3. token-group scan in LDS -> tile aggregate, published;
+//   4. look-back -> carry-in;
+//   5. pass 2: replay s = lam*s + w from the carry, store out.
 // All tensor traffic uses buffer descriptors (osm_device.h): no per-element
-// address arithmetic, no bounds branches.
-#include <stdlib.h>
-
-#include <mutex>
-#include <string>
-#include <unordered_map>
-
+// address arithmetic and no bounds branches.
 #include "osm_chain.h"
 
 namespace osm {
 namespace {
 
-template <bool DYN>
-using Geo = FwdGeoT<DYN>;
-
-// Fast path: w = (1 - lam) * tanh(damping * p) with c pre-scaled by
-// 2*log2(e)*damping.  softsign as copysign(1 - 1/(1 + |x|), x): +-Inf and
-// huge |x| give +-1 (the reciprocal underflows to 0), and a NaN x yields a
-// NaN w, so runs containing one are recomputed by ema_input_exact
-// (NaN x -> w = 0 as sdpc_kernel.py:2086).  Absolute error of u ~ 6e-8.
+// Exact input for the rare path (see pass1_exact): NaN x -> w = 0 as
+// sdpc_kernel.py:2086, +-Inf -> u = +-1.
 template <int KP>
-__device__ __forceinline__ float ema_input_fast(float x, const float* c, float one_m, float neg2_one_m) {
-  const float u = __builtin_copysignf(1.0f - __builtin_amdgcn_rcpf(1.0f + __builtin_fabsf(x)), x);
-  const float r = tanh_r(clenshaw<KP>(u, c));
-  return __builtin_fmaf(neg2_one_m, r, one_m);
-}
-
-template <int KP>
-__device__ __forceinline__ float ema_input_exact(float x, const float* c, float one_m, float neg2_one_m) {
-  const float r = tanh_r(clenshaw<KP>(softsign(x), c));
+__device__ __forceinline__ float ema_input_exact(float x, const float (&a)[KP], float one_m, float neg2_one_m) {
+  const float r = tanh_r(horner<KP>(softsign(x), a));
   const float w = __builtin_fmaf(neg2_one_m, r, one_m);
   return (x == x) ? w : 0.0f;
 }
 
 // Descriptors of one tile and this thread's offsets into them.
-template <bool DYN, typename XT, typename OT>
 struct TileAddr {
   Rsrc x, out, g, c;
-  uint32_t vx, vo, vg, vc;   // per-thread byte offsets (kOffOOB: lanes >= D)
+  uint32_t vx, vo, vg;       // per-thread byte offsets (kOffOOB: lanes >= D)
   uint32_t sx, so, sg, sc;   // uniform byte steps: one token (x, out, g), one k (coeffs)
   int h;
 };
 
-template <bool DYN, typename XT, typename OT>
-__device__ __forceinline__ TileAddr<DYN, XT, OT> tile_addr(const FwdParams& p, const ThreadPos& q,
-                                                           const TileInfo& ti) {
-  TileAddr<DYN, XT, OT> a;
-  const int t_tile = ti.tile * Geo<DYN>::TILE;
-  const int d0 = ti.lbd * kLanes + q.lt * Geo<DYN>::LPT;
+template <class G, bool DYN, typename XT, typename OT>
+__device__ __forceinline__ TileAddr tile_addr(const FwdParams& p, const ThreadPos& q, const TileInfo& ti) {
+  TileAddr a;
+  const int t_tile = ti.tile * G::TILE;
+  const int d0 = ti.lbd * kLanes + q.lt * G::LPT;
   const bool lane_ok = d0 < p.D;
   const uint64_t rows_after = (uint64_t)(p.S - 1 - t_tile);
   a.h = lane_ok ? d0 / p.hd : 0;
-  const int j0 = d0 - a.h * p.hd;
-  const int64_t row0 = (int64_t)q.tg * Geo<DYN>::R;
+  const int64_t row0 = (int64_t)q.tg * G::R;
   // x and out: the extent ends after row S-1, so padding rows read 0 and
   // their stores are dropped.
   const char* xb = static_cast<const char*>(p.x) + ((int64_t)ti.b * p.x_sb + (int64_t)t_tile * p.x_ss) * sizeof(XT);
@@ -92,294 +66,261 @@ __device__ __forceinline__ TileAddr<DYN, XT, OT> tile_addr(const FwdParams& p, c
   const char* cb = reinterpret_cast<const char*>(p.coeffs) + (int64_t)ti.b * p.c_sb * 4;
   a.c = make_rsrc(cb, kMaxExtent);
   a.sc = (uint32_t)(p.c_sk * 4);
-  a.vc = lane_ok ? (uint32_t)(((int64_t)a.h * p.c_sh + j0) * 4) : kOffOOB;
   return a;
 }
 
-// Registers holding one tile's inputs for this thread.
-template <bool DYN, int KP>
-struct TileInputs {
-  float x[Geo<DYN>::R][Geo<DYN>::LPT];
-  float g[DYN ? Geo<DYN>::R : 1];
-  float c[Geo<DYN>::LPT][KP];   // raw coefficients (0 beyond K and for lanes >= D)
-  float lam, damp;
-};
-
 // Advances a uniform byte offset by `step` in a way the compiler cannot fold:
-// otherwise every r * step product is hoisted out of the tile loop and held
-// in its own SGPR for the whole kernel.
+// otherwise every r * step product is materialised in its own SGPR.
 __device__ __forceinline__ uint32_t next_off(uint32_t off, uint32_t step) {
   off += step;
   asm volatile("" : "+s"(off));
   return off;
 }
 
-template <bool DYN, typename XT, typename OT, int KP>
-__device__ __forceinline__ void load_tile(TileInputs<DYN, KP>& in, const FwdParams& p,
-                                          const TileAddr<DYN, XT, OT>& a) {
-  uint32_t so = 0;
-#pragma unroll
-  for (int r = 0; r < Geo<DYN>::R; ++r) {
-    BufVec<XT, Geo<DYN>::LPT>::load(a.x, a.vx, so, in.x[r]);
-    so = next_off(so, a.sx);
-  }
-  if constexpr (DYN) {
-    uint32_t sg = 0;
-#pragma unroll
-    for (int r = 0; r < Geo<DYN>::R; ++r) {
-      float gv[1];
-      BufVec<float, 1>::load(a.g, a.vg, sg, gv);
-      in.g[r] = gv[0];
-      sg = next_off(sg, a.sg);
-    }
-  }
-  uint32_t sc = 0;
-#pragma unroll
-  for (int k = 0; k < KP; ++k) {
-    float cv[Geo<DYN>::LPT];
-    if (k < p.K) {
-      BufVec<float, Geo<DYN>::LPT>::load(a.c, a.vc, sc, cv);
-      sc = next_off(sc, a.sc);
-    } else {
-#pragma unroll
-      for (int i = 0; i < Geo<DYN>::LPT; ++i) cv[i] = 0.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < Geo<DYN>::LPT; ++i) in.c[i][k] = cv[i];
-  }
-  in.lam = p.lam[a.h];
-  in.damp = p.damping[a.h];
-}
-
-// Pass 1 over this thread's run: w (in place of x) and the run aggregate.
-// Tokens >= S in the last tile read x = 0 and are processed like the others:
-// they only feed the last tile's own aggregate (never published) and the
-// carries of later, equally padded, token groups, whose stores are dropped.
-template <bool DYN, int KP>
-__device__ __forceinline__ void pass1(TileInputs<DYN, KP>& in, const FwdParams& p, const float (&c)[Geo<DYN>::LPT][KP],
-                                      float (&lamv)[DYN ? Geo<DYN>::R : 1], float& A, float (&Bv)[Geo<DYN>::LPT]) {
-  A = 1.0f;
-#pragma unroll
-  for (int i = 0; i < Geo<DYN>::LPT; ++i) Bv[i] = 0.0f;
-#pragma unroll
-  for (int r = 0; r < Geo<DYN>::R; ++r) {
-    float lam = in.lam;
-    if constexpr (DYN) {
-      lam = __builtin_amdgcn_fmed3f(__builtin_fmaf(p.lam_shift, in.g[r], in.lam), p.lam_min, p.lam_max);
-      lamv[r] = lam;
-    }
-    const float one_m = 1.0f - lam;
-    const float n2 = -2.0f * one_m;
-#pragma unroll
-    for (int i = 0; i < Geo<DYN>::LPT; ++i) {
-      const float w = ema_input_fast<KP>(in.x[r][i], c[i], one_m, n2);
-      in.x[r][i] = w;
-      Bv[i] = __builtin_fmaf(lam, Bv[i], w);
-    }
-    A *= lam;
-  }
-}
-
 // Rare path: a run whose aggregate is NaN saw a NaN or infinite input (or
 // non-finite coefficients).  Reload its x and recompute with the exact
 // special-value handling.
-template <bool DYN, typename XT, typename OT, int KP>
-__device__ __forceinline__ void pass1_exact(TileInputs<DYN, KP>& in, const FwdParams& p, const TileAddr<DYN, XT, OT>& a,
-                                         const float (&c)[Geo<DYN>::LPT][KP], const float (&lamv)[DYN ? Geo<DYN>::R : 1],
-                                         float (&Bv)[Geo<DYN>::LPT]) {
+template <class G, bool DYN, typename XT, int KP>
+__device__ __forceinline__ void pass1_exact(float (&w)[G::R][G::LPT], const TileAddr& a, const float (&c)[G::LPT][KP],
+                                            const float (&lamv)[G::R], float (&Bv)[G::LPT]) {
 #pragma unroll
-  for (int i = 0; i < Geo<DYN>::LPT; ++i) Bv[i] = 0.0f;
-  for (int r = 0; r < Geo<DYN>::R; ++r) {
-    float xv[Geo<DYN>::LPT];
-    BufVec<XT, Geo<DYN>::LPT>::load(a.x, a.vx, (uint32_t)r * a.sx, xv);
-    const float lam = DYN ? lamv[r] : in.lam;
+  for (int i = 0; i < G::LPT; ++i) Bv[i] = 0.0f;
+  for (int r = 0; r < G::R; ++r) {
+    float xv[G::LPT];
+    BufVec<XT, G::LPT>::load(a.x, a.vx, (uint32_t)r * a.sx, xv);
+    const float lam = lamv[r];
     const float one_m = 1.0f - lam;
     const float n2 = -2.0f * one_m;
 #pragma unroll
-    for (int i = 0; i < Geo<DYN>::LPT; ++i) {
-      const float w = ema_input_exact<KP>(xv[i], c[i], one_m, n2);
-      in.x[r][i] = w;
-      Bv[i] = __builtin_fmaf(lam, Bv[i], w);
+    for (int i = 0; i < G::LPT; ++i) {
+      w[r][i] = ema_input_exact<KP>(xv[i], c[i], one_m, n2);
+      Bv[i] = __builtin_fmaf(lam, Bv[i], w[r][i]);
     }
   }
 }
 
-// PERSIST: persistent blocks taking tiles by class tickets, with the next
-// tile prefetched; otherwise one tile per block (v = blockIdx.x).
-template <bool DYN, typename XT, typename OT, int KP, bool PERSIST>
-__global__ void __launch_bounds__(Geo<DYN>::THREADS) cheby_ema_fwd_kernel(const FwdParams p) {
-  using G = Geo<DYN>;
-  constexpr int R = Geo<DYN>::R;
-  constexpr int LPT = Geo<DYN>::LPT;
+// Pass 2 over a thread's run: s = lam*s + w from the carried state, out =
+// clamp(s, lo, hi).  FINAL: also stores the state at run index r_fin to fin
+// (when fin is non-NULL).
+template <class G, typename OT, bool FINAL>
+__device__ __forceinline__ void pass2(float (&s)[G::LPT], const float (&w)[G::R][G::LPT], const float (&lamv)[G::R],
+                                      const TileAddr& a, float lo, float hi, int r_fin, float* fin) {
+  uint32_t so = 0;
+#pragma unroll
+  for (int r = 0; r < G::R; ++r) {
+    float o[G::LPT];
+#pragma unroll
+    for (int i = 0; i < G::LPT; ++i) {
+      s[i] = __builtin_fmaf(lamv[r], s[i], w[r][i]);
+      o[i] = __builtin_amdgcn_fmed3f(s[i], lo, hi);
+    }
+    if constexpr (FINAL) {
+      if (r == r_fin && fin) {
+#pragma unroll
+        for (int i = 0; i < G::LPT; ++i) fin[i] = s[i];
+      }
+    }
+    BufVec<OT, G::LPT>::store(a.out, a.vo, so, o);
+    so = next_off(so, a.so);
+  }
+}
+
+// Two workgroups (4 waves per SIMD) per CU: at most 128 VGPRs.
+template <class G, bool DYN, typename XT, typename OT, int KP>
+__global__ void __launch_bounds__(G::THREADS) __attribute__((amdgpu_waves_per_eu(4)))
+cheby_ema_fwd_kernel(const FwdParams p) {
+  constexpr int R = G::R;
+  constexpr int LPT = G::LPT;
   constexpr int WORDS = DYN ? 2 : 1;
   __shared__ ChainLds<G> L;
 
   const ThreadPos q = thread_pos<G>();
   const Tags tags = launch_tags(p.hdr);
-  const int cls = blockIdx.x & 7;
-  const int n_virt = p.n_lb_pad * p.n_tiles;
+  const TileInfo ti = tile_info(blockIdx.x, p.n_lb, p.n_lb_pad, p.n_lbd, p.n_tiles);
+  if (ti.pad) {
+    finish_block(p.hdr, tags.epoch);
+    return;
+  }
+  const TileAddr a = tile_addr<G, DYN, XT, OT>(p, q, ti);
 
-  int v;
-  if constexpr (PERSIST) {
-    if (q.tid == 0) L.next_v = ticket_to_tile(take_ticket(p.hdr, cls), cls, p.n_lb, p.n_lb_pad, p.n_tiles);
-    __syncthreads();
-    v = L.next_v;
-    __syncthreads();  // everyone has read next_v before thread 0 rewrites it
-  } else {
-    v = blockIdx.x;
-    if (v % p.n_lb_pad >= p.n_lb) v = n_virt;  // padding block: nothing to do
+  // Monomial coefficients of the series for the tile's 64 lanes, scaled by
+  // 2*log2(e)*damping (the tanh argument in exp2 units): wave j < KP forms
+  // coefficient j of every lane from <= 4 Chebyshev coefficients in float64
+  // and shares it through LDS.  Its loads are issued before those of x so
+  // that the conversion only waits for them.
+  static_assert(KP <= G::WAVES && KP <= 8, "one wave per monomial coefficient");
+  __shared__ float mono[KP][kLanes];
+  const int jw = __builtin_amdgcn_readfirstlane(q.wave);
+  float cm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float kap_l = 0.0f;
+  if (jw < KP) {
+    const int d = ti.lbd * kLanes + q.wl;
+    const bool ok = d < p.D;
+    const int h = ok ? d / p.hd : 0;
+    const uint32_t vc = ok ? (uint32_t)(((int64_t)h * p.c_sh + (d - h * p.hd)) * 4) : kOffOOB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = jw + 2 * i;
+      float v[1];
+      BufVec<float, 1>::load(a.c, k < p.K ? vc : kOffOOB, (uint32_t)k * a.sc, v);
+      cm[i] = v[0];
+    }
+    kap_l = kTwoLog2e * p.damping[h];
   }
 
-  TileInputs<DYN, KP> in;
-  TileAddr<DYN, XT, OT> a;
-  if (v < n_virt) {
-    a = tile_addr<DYN, XT, OT>(p, q, tile_info(v, p.n_lb, p.n_lb_pad, p.n_lbd, p.n_tiles));
-    load_tile<DYN, XT, OT, KP>(in, p, a);
-  }
-
-  while (v < n_virt) {
-    const TileInfo ti = tile_info(v, p.n_lb, p.n_lb_pad, p.n_lbd, p.n_tiles);
-    const TileAddr<DYN, XT, OT> cur = a;
-    unsigned pending = 0;
-    if (PERSIST && q.tid == 0) pending = take_ticket(p.hdr, cls);   // waited for only after pass 1
-
-    // Pass 1.
-    const float lam_h = in.lam;
-    float lamv[DYN ? R : 1];
-    float A, Bv[LPT];
-    float c[LPT][KP];
-    {
-      const float kap = kTwoLog2e * in.damp;
-#pragma unroll
-      for (int i = 0; i < LPT; ++i)
-#pragma unroll
-        for (int k = 0; k < KP; ++k) c[i][k] = kap * in.c[i][k];
-    }
-    pass1<DYN, KP>(in, p, c, lamv, A, Bv);
-    bool bad = false;
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) bad |= Bv[i] != Bv[i];
-    if (bad) pass1_exact<DYN, XT, OT, KP>(in, p, cur, c, lamv, Bv);
-    if (PERSIST && q.tid == 0) L.next_v = ticket_to_tile(pending, cls, p.n_lb, p.n_lb_pad, p.n_tiles);
-
-    unsigned long long* lane_slots = p.slots + ((size_t)ti.lb * p.n_tiles * kLanes + q.wl) * WORDS;
-    const size_t tile_stride = (size_t)kLanes * WORDS;
-    float pA, pB[LPT], aggA, aggB;
-    tile_scan<G, DYN>(L, q, ti, tags, A, Bv, pA, pB, aggA, aggB, lane_slots, tile_stride);
-    const int vn = PERSIST ? L.next_v : n_virt;
-
-    const int dl = ti.lbd * kLanes + q.wl;
-    const bool dl_ok = dl < p.D;
-    const float init_wl = (p.ema_init && dl_ok) ? p.ema_init[(int64_t)ti.b * p.D + dl] : 0.0f;
-    const float lam_wl = DYN ? 0.0f : p.lam[dl_ok ? dl / p.hd : 0];
-    LookBack<G, DYN> lbk;
-    look_back_issue<G, DYN>(lbk, q, ti, lane_slots, tile_stride);
-    // Move the current tile's w out of the prefetch registers, then prefetch.
-    float w[R][LPT];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int i = 0; i < LPT; ++i) w[r][i] = in.x[r][i];
-    if (PERSIST && vn < n_virt) {
-      a = tile_addr<DYN, XT, OT>(p, q, tile_info(vn, p.n_lb, p.n_lb_pad, p.n_lbd, p.n_tiles));
-      load_tile<DYN, XT, OT, KP>(in, p, a);
-    }
-    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, lane_slots, tile_stride, init_wl, lam_wl, p.hdr);
-
-    // Pass 2: replay the recurrence from the true carry and store out.
-    float s[LPT];
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) s[i] = __builtin_fmaf(pA, L.carry[q.lt * LPT + i], pB[i]);
-    const int t0 = ti.tile * Geo<DYN>::TILE + q.tg * R;
-    const int r_last = p.S - 1 - t0;   // run index of token S-1 (in range only for one run)
-    float s_last[LPT];
+  // x rows of this thread's run, g (dynamic lambda).
+  float w[R][LPT];
+  {
     uint32_t so = 0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const float lam = DYN ? lamv[r] : lam_h;
-      float o[LPT];
+      BufVec<XT, LPT>::load(a.x, a.vx, so, w[r]);
+      so = next_off(so, a.sx);
+    }
+  }
+  const float lam_h = p.lam[a.h];
+  float lamv[R];
+  if constexpr (DYN) {
+    uint32_t sg = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float gv[1];
+      BufVec<float, 1>::load(a.g, a.vg, sg, gv);
+      lamv[r] = gv[0];
+      sg = next_off(sg, a.sg);
+    }
+  }
+
+  if (jw < KP) {
+    double acc = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = __builtin_fma((double)kChebMono[jw][i], (double)cm[i], acc);
+    mono[jw][q.wl] = (float)(acc * (double)kap_l);
+  }
+  __syncthreads();
+  float c[LPT][KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j)
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) c[i][j] = mono[j][q.lt * LPT + i];
+
+  // Pass 1: w = (1 - lam) * tanh(damping * p(u)) in place of x, and the run
+  // aggregate (A, B) from a zero state.  softsign as copysign(1 - 1/(1+|x|), x):
+  // +-Inf and huge |x| give +-1 (the reciprocal underflows to 0; absolute
+  // error of u ~ 6e-8); a NaN x yields a NaN w, so a run containing one is
+  // recomputed by pass1_exact.  tanh as 1 - 2/(1 + exp2(y)) with y from the
+  // pre-scaled coefficients.  Tokens >= S of the last tile read x = 0 and are
+  // processed like the others: they only feed the last tile's own aggregate
+  // (never published) and the carries of later, equally padded, token groups.
+  float A = 1.0f;
+  float Bv[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) Bv[i] = 0.0f;
+  // kRB rows at a time, the polynomial steps interleaved across the rows'
+  // elements: each Horner step depends on the previous one, so independent
+  // chains keep the VALU pipeline busy.
+  constexpr int kRB = 2;
+  static_assert(R % kRB == 0, "row block");
+#pragma unroll
+  for (int r0 = 0; r0 < R; r0 += kRB) {
+    float u[kRB][LPT], py[kRB][LPT];
+#pragma unroll
+    for (int rr = 0; rr < kRB; ++rr) {
+      float lam = lam_h;
+      if constexpr (DYN)
+        lam = __builtin_amdgcn_fmed3f(__builtin_fmaf(p.lam_shift, lamv[r0 + rr], lam_h), p.lam_min, p.lam_max);
+      lamv[r0 + rr] = lam;
 #pragma unroll
       for (int i = 0; i < LPT; ++i) {
-        s[i] = __builtin_fmaf(lam, s[i], w[r][i]);
-        o[i] = p.clamp_out ? __builtin_amdgcn_fmed3f(s[i], -1.0f, 1.0f) : s[i];
+        const float x = w[r0 + rr][i];
+        u[rr][i] = __builtin_copysignf(1.0f - __builtin_amdgcn_rcpf(1.0f + __builtin_fabsf(x)), x);
+        py[rr][i] = c[i][KP - 1];
       }
-      if (ti.is_last && r == r_last) {
+    }
 #pragma unroll
-        for (int i = 0; i < LPT; ++i) s_last[i] = s[i];
+    for (int j = KP - 2; j >= 0; --j)
+#pragma unroll
+      for (int rr = 0; rr < kRB; ++rr)
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) py[rr][i] = __builtin_fmaf(py[rr][i], u[rr][i], c[i][j]);
+#pragma unroll
+    for (int rr = 0; rr < kRB; ++rr) {
+      const float lam = lamv[r0 + rr];
+      const float one_m = 1.0f - lam;
+      const float n2 = -2.0f * one_m;
+#pragma unroll
+      for (int i = 0; i < LPT; ++i) {
+        w[r0 + rr][i] = __builtin_fmaf(n2, tanh_r(py[rr][i]), one_m);
+        Bv[i] = __builtin_fmaf(lam, Bv[i], w[r0 + rr][i]);
       }
-      BufVec<OT, LPT>::store(cur.out, cur.vo, so, o);
-      so = next_off(so, cur.so);
+      A *= lam;
     }
-    // ema_final = unclamped state at token S-1, from the run that holds it.
-    if (ti.is_last && r_last >= 0 && r_last < R && cur.vo != kOffOOB && p.ema_final) {
-      const int d0 = ti.lbd * kLanes + q.lt * LPT;
+  }
+  bool bad = false;
 #pragma unroll
-      for (int i = 0; i < LPT; ++i) p.ema_final[(int64_t)ti.b * p.D + d0 + i] = s_last[i];
-    }
-    v = vn;
+  for (int i = 0; i < LPT; ++i) bad |= Bv[i] != Bv[i];
+  if (bad) pass1_exact<G, DYN, XT, KP>(w, a, c, lamv, Bv);
+
+  unsigned long long* lane_slots = p.slots + ((size_t)ti.lb * p.n_tiles * kLanes + q.wl) * WORDS;
+  const size_t tile_stride = (size_t)kLanes * WORDS;
+  float pA, pB[LPT], aggA, aggB;
+  tile_scan<G, DYN>(L, q, ti, tags, A, Bv, pA, pB, aggA, aggB, lane_slots, tile_stride);
+
+  const int dl = ti.lbd * kLanes + q.wl;
+  const bool dl_ok = dl < p.D;
+  const float init_wl = (p.ema_init && dl_ok) ? p.ema_init[(int64_t)ti.b * p.D + dl] : 0.0f;
+  const float lam_wl = DYN ? 0.0f : p.lam[dl_ok ? dl / p.hd : 0];
+  {
+    LookBack<G, DYN> lbk;
+    look_back_issue<G, DYN>(lbk, q, ti, lane_slots, tile_stride);
+    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, lane_slots, tile_stride, init_wl, lam_wl, p.hdr);
+  }
+
+  // Pass 2: replay the recurrence from the true carry and store out.
+  float s[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) s[i] = __builtin_fmaf(pA, L.carry[q.lt * LPT + i], pB[i]);
+  const float lo = p.clamp_out ? -1.0f : -__builtin_inff();
+  const float hi = p.clamp_out ? 1.0f : __builtin_inff();
+  if (!ti.is_last) {
+    pass2<G, OT, false>(s, w, lamv, a, lo, hi, 0, nullptr);
+  } else {
+    // The last tile also yields ema_final: the unclamped state at token S-1,
+    // from the one run that holds it.
+    const int r_last = p.S - 1 - (ti.tile * G::TILE + q.tg * R);
+    float* fin = (p.ema_final && a.vo != kOffOOB && r_last >= 0 && r_last < R)
+                     ? p.ema_final + (int64_t)ti.b * p.D + ti.lbd * kLanes + q.lt * LPT
+                     : nullptr;
+    pass2<G, OT, true>(s, w, lamv, a, lo, hi, r_last, fin);
   }
   finish_block(p.hdr, tags.epoch);
 }
 
-// Blocks that can be resident at once for `fn` on the current device.
-int resident_blocks(const void* fn, int threads) {
-  static std::mutex mu;
-  static std::unordered_map<uint64_t, int> cache;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  const uint64_t key = ((uint64_t)(uintptr_t)fn << 8) ^ (uint64_t)dev;
-  {
-    std::lock_guard<std::mutex> lk(mu);
-    auto it = cache.find(key);
-    if (it != cache.end()) return it->second;
-  }
-  int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0) != hipSuccess || per_cu < 1) per_cu = 1;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
-  const int n = per_cu * cus;
-  std::lock_guard<std::mutex> lk(mu);
-  cache[key] = n;
-  return n;
-}
-
-// Schedule of the forward kernel: OSM_FWD_SCHEDULE=persistent|oneshot
-// (default oneshot).  Both produce identical results.
-bool persistent_schedule() {
-  static const bool v = [] {
-    const char* e = getenv("OSM_FWD_SCHEDULE");
-    return e && std::string(e) == "persistent";
-  }();
-  return v;
-}
-
-template <bool DYN, typename XT, typename OT, int KP>
-hipError_t launch_one(const FwdParams& p, hipStream_t stream) {
-  const int n_virt = p.n_lb_pad * p.n_tiles;
-  if (persistent_schedule()) {
-    const void* fn = reinterpret_cast<const void*>(&cheby_ema_fwd_kernel<DYN, XT, OT, KP, true>);
-    int grid = resident_blocks(fn, Geo<DYN>::THREADS);
-    grid = grid < n_virt ? grid : n_virt;
-    grid = grid / 8 * 8;
-    if (grid < 8) grid = 8;
-    hipLaunchKernelGGL((cheby_ema_fwd_kernel<DYN, XT, OT, KP, true>), dim3(grid), dim3(Geo<DYN>::THREADS), 0, stream, p);
-  } else {
-    hipLaunchKernelGGL((cheby_ema_fwd_kernel<DYN, XT, OT, KP, false>), dim3(n_virt), dim3(Geo<DYN>::THREADS), 0, stream,
-                       p);
-  }
+template <class G, bool DYN, typename XT, typename OT>
+hipError_t launch_g(const FwdParams& p, int kpad, hipStream_t stream) {
+  const unsigned grid = (unsigned)p.n_lb_pad * (unsigned)p.n_tiles;
+  if (kpad == 4)
+    hipLaunchKernelGGL((cheby_ema_fwd_kernel<G, DYN, XT, OT, 4>), dim3(grid), dim3(G::THREADS), 0, stream, p);
+  else
+    hipLaunchKernelGGL((cheby_ema_fwd_kernel<G, DYN, XT, OT, 8>), dim3(grid), dim3(G::THREADS), 0, stream, p);
   return hipGetLastError();
 }
 
 template <bool DYN, typename XT, typename OT>
-hipError_t launch_k(const FwdParams& p, int kpad, hipStream_t stream) {
-  return kpad == 4 ? launch_one<DYN, XT, OT, 4>(p, stream) : launch_one<DYN, XT, OT, 8>(p, stream);
+hipError_t launch_k(const FwdParams& p, int tile, int kpad, hipStream_t stream) {
+  if constexpr (!DYN) {
+    if (tile == FwdTileLarge::TILE) return launch_g<FwdTileLarge, DYN, XT, OT>(p, kpad, stream);
+  }
+  if (tile == FwdTileMedium::TILE) return launch_g<FwdTileMedium, DYN, XT, OT>(p, kpad, stream);
+  return launch_g<FwdTileSmall, DYN, XT, OT>(p, kpad, stream);
 }
 
 template <bool DYN>
-hipError_t launch_dt(const FwdParams& p, int x_dtype, int out_dtype, int kpad, hipStream_t stream) {
-  if (x_dtype == 0 && out_dtype == 0) return launch_k<DYN, float, float>(p, kpad, stream);
-  if (x_dtype == 0 && out_dtype == 1) return launch_k<DYN, float, __bf16>(p, kpad, stream);
-  if (x_dtype == 1 && out_dtype == 0) return launch_k<DYN, __bf16, float>(p, kpad, stream);
-  return launch_k<DYN, __bf16, __bf16>(p, kpad, stream);
+hipError_t launch_dt(const FwdParams& p, int x_dtype, int out_dtype, int tile, int kpad, hipStream_t stream) {
+  if (x_dtype == 0 && out_dtype == 0) return launch_k<DYN, float, float>(p, tile, kpad, stream);
+  if (x_dtype == 0 && out_dtype == 1) return launch_k<DYN, float, __bf16>(p, tile, kpad, stream);
+  if (x_dtype == 1 && out_dtype == 0) return launch_k<DYN, __bf16, float>(p, tile, kpad, stream);
+  return launch_k<DYN, __bf16, __bf16>(p, tile, kpad, stream);
 }
 
 // Grid-stride zero fill (graph-capturable, unlike hipMemsetAsync nodes).
@@ -395,15 +336,27 @@ __global__ void copy_state_kernel(const float* src, float* dst, size_t n) {
 
 }  // namespace
 
+int fwd_tile_tokens(bool dyn, int64_t n_lb, int64_t S) {
+  // Largest tile that still leaves >= kMinTiles workgroups (2 per CU on a
+  // 256-CU MI355X, the residency of the large tile); dynamic lambda holds
+  // more per-token state, so at most the medium tile.
+  constexpr int64_t kMinTiles = 512;
+  const int64_t n_pad = (n_lb + 7) / 8 * 8;
+  if (!dyn && n_pad * ((S + FwdTileLarge::TILE - 1) / FwdTileLarge::TILE) >= kMinTiles) return FwdTileLarge::TILE;
+  if (n_pad * ((S + FwdTileMedium::TILE - 1) / FwdTileMedium::TILE) >= kMinTiles) return FwdTileMedium::TILE;
+  return FwdTileSmall::TILE;
+}
+
 size_t slot_words(bool dyn) { return dyn ? 2 : 1; }
 
 size_t fwd_workspace_bytes(int n_lb, int n_tiles, bool dyn) {
   return kHeaderBytes + (size_t)n_lb * (size_t)n_tiles * kLanes * slot_words(dyn) * 8;
 }
 
-hipError_t launch_fwd(const FwdParams& p, int x_dtype, int out_dtype, bool dyn, int kpad, hipStream_t stream) {
-  return dyn ? launch_dt<true>(p, x_dtype, out_dtype, kpad, stream)
-             : launch_dt<false>(p, x_dtype, out_dtype, kpad, stream);
+hipError_t launch_fwd(const FwdParams& p, int x_dtype, int out_dtype, bool dyn, int tile, int kpad,
+                      hipStream_t stream) {
+  return dyn ? launch_dt<true>(p, x_dtype, out_dtype, tile, kpad, stream)
+             : launch_dt<false>(p, x_dtype, out_dtype, tile, kpad, stream);
 }
 
 hipError_t launch_fill_zero(void* ptr, size_t bytes, hipStream_t stream) {

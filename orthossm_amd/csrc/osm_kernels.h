@@ -30,12 +30,17 @@ struct TileGeo {
   static_assert(64 % LPT == 0 && 64 % WAVES == 0, "geometry");
 };
 
-// Forward: 2 lanes per thread, 8 waves.  Static lambda: 32-token runs
-// (512-token tiles); dynamic lambda keeps a per-token lambda and g in
-// registers, so 16-token runs (256-token tiles).  Chosen by measurement on
-// MI355X at BASELINE configs[1] and configs[3].
-template <bool DYN>
-using FwdGeoT = typename std::conditional<DYN, TileGeo<2, 8, 16>, TileGeo<2, 8, 32>>::type;
+// Forward: 2 lanes per thread, 8 waves; the run length sets the tile.
+// Longer runs amortise the per-tile scan and look-back over more tokens but
+// give fewer workgroups, so the host takes the largest tile that still fills
+// the chip (fwd_tile_tokens).  Dynamic lambda keeps a per-token lambda in
+// registers and is limited to the medium tile.
+using FwdTileLarge = TileGeo<2, 8, 32>;    // 512 tokens
+using FwdTileMedium = TileGeo<2, 8, 16>;   // 256 tokens
+using FwdTileSmall = TileGeo<2, 8, 8>;     // 128 tokens
+constexpr int kMaxFwdTile = FwdTileLarge::TILE;
+// Tokens per forward tile for a launch with n_lb lane-blocks over S tokens.
+int fwd_tile_tokens(bool dyn, int64_t n_lb, int64_t S);
 // TTT: keeps x, r and dL/ds per token in registers -> shorter runs.
 using TttGeo = TileGeo<2, 8, 8>;
 
@@ -75,7 +80,7 @@ size_t fwd_workspace_bytes(int n_lb, int n_tiles, bool dyn);
 size_t ttt_workspace_bytes(int n_lb, int n_tiles, bool dyn, int K);
 
 // Launchers: return hipSuccess or the launch error.
-hipError_t launch_fwd(const FwdParams& p, int x_dtype, int out_dtype, bool dyn, int kpad,
+hipError_t launch_fwd(const FwdParams& p, int x_dtype, int out_dtype, bool dyn, int tile, int kpad,
                       hipStream_t stream);
 hipError_t launch_ttt(const FwdParams& p, float* grad, int x_dtype, int out_dtype, bool dyn,
                       int kpad, hipStream_t stream);
