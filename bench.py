@@ -7,12 +7,17 @@ Default workload: BASELINE configs[1] ("headline"): B=4, S=16384, D=512
 the fused operator over one batch held in HBM.  Inputs rotate over 4
 buffer sets (>1 GB) so the 256 MB Infinity Cache cannot serve them.
 
-Prints ONE JSON line (rank 0).  ``roofline`` prices the dominant kernel
-against HBM: achieved = algorithmic bytes per launch (every input read once,
-every output written once) / average kernel duration measured with HIP
-events on the stream the kernel is launched on.  ``cpu_baseline`` times the
-CPU restatement of the reference's PyTorch path (oracle/reference_form.py)
-on this host's cores, on a bounded sample (one batch row).
+Prints ONE JSON line (rank 0).  The timed region is exactly K steps
+back to back between two HIP events on the stream the kernels run on.
+``roofline`` prices the fused operator against HBM: achieved = algorithmic
+bytes per launch (every input read once, every output written once) / the
+average launch duration over that region (a step is one launch, or one per
+chunk for the streaming workload; the TTT step's two small merge kernels,
+~2% of it, are counted in).  ``traffic`` is the HBM bytes per launch of the
+main kernel measured with rocprofv3 counters (profiles/hbm_traffic.json).
+``cpu_baseline`` times the CPU restatement of the reference's PyTorch path
+(oracle/reference_form.py) on this host's cores, on a bounded sample (one
+batch row).
 """
 from __future__ import annotations
 
@@ -46,10 +51,8 @@ def algorithmic_bytes(cfg) -> int:
     total += 2 * cfg.H * 4                               # damping, lambda
     if cfg.dynamic:
         total += cfg.B * cfg.S * cfg.H * 4               # g [B,S,H]
-    if cfg.chunk:
-        total += 2 * cfg.B * cfg.D * 4 * (cfg.S // cfg.chunk)   # state in/out per chunk
-    else:
-        total += cfg.B * cfg.D * 4                       # ema_final
+    launches = cfg.S // cfg.chunk if cfg.chunk else 1
+    total += 2 * cfg.B * cfg.D * 4 * launches            # ema_init in, ema_final out per launch
     if cfg.ttt:
         total += cfg.B * cfg.H * cfg.K * cfg.hd * 4      # grad
     return total
@@ -88,11 +91,61 @@ def cpu_baseline(cfg):
 
 
 def measured_traffic(workload: str):
+    """HBM bytes per launch (read + write) from profiles/hbm_traffic.json."""
     try:
         with open(TRAFFIC_FILE) as f:
-            return json.load(f).get(workload)
-    except (OSError, ValueError):
+            entry = json.load(f).get(workload)
+        return None if entry is None else entry["bytes"]
+    except (OSError, ValueError, KeyError):
         return None
+
+
+def _counter_rows(path: str, counter: str):
+    import csv
+    import glob
+    files = [path] if os.path.isfile(path) else glob.glob(os.path.join(path, "**", "*counter_collection.csv"),
+                                                            recursive=True)
+    rows = []
+    for fn in files:
+        with open(fn) as f:
+            rows += [r for r in csv.DictReader(f) if r["Counter_Name"] == counter]
+    return sorted(rows, key=lambda r: int(r["Dispatch_Id"]))
+
+
+def pmc_summary(fetch_path: str, write_path: str, workload: str) -> dict:
+    """HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc
+    runs of ``bench.py --calibrate-copy`` (FETCH_SIZE, then WRITE_SIZE, KiB
+    per dispatch).  Each counter is scaled by bytes/counter of the run's last
+    5 copy kernels (plain device copies of one x buffer, size known), then
+    stored under ``workload`` in profiles/hbm_traffic.json."""
+    cfg = CONFIGS[workload]
+    copy_bytes = cfg.B * cfg.S * cfg.D * (2 if cfg.dtype == torch.bfloat16 else 4)
+    out = {}
+    for key, counter, path in (("read", "FETCH_SIZE", fetch_path), ("write", "WRITE_SIZE", write_path)):
+        rows = _counter_rows(path, counter)
+        ours = [float(r["Counter_Value"]) * 1024 for r in rows
+                if "cheby_ema_fwd_kernel" in r["Kernel_Name"] or "cheby_ema_ttt_kernel" in r["Kernel_Name"]]
+        copies = [float(r["Counter_Value"]) * 1024 for r in rows if "copyBuffer" in r["Kernel_Name"]][-5:]
+        if not ours or len(copies) < 5:
+            raise SystemExit(f"pmc_summary: {path} lacks kernel or 5 calibration copies for {counter}")
+        scale = copy_bytes / (sum(copies) / len(copies))
+        out[f"{key}_bytes"] = scale * sum(ours) / len(ours)
+        out[f"{key}_counter_kib"] = sum(ours) / len(ours) / 1024
+        out[f"{key}_scale"] = scale
+        out[f"{key}_dispatches"] = len(ours)
+    out["bytes"] = out["read_bytes"] + out["write_bytes"]
+    out["algorithmic_bytes"] = algorithmic_bytes(cfg) / (cfg.S // cfg.chunk if cfg.chunk else 1)
+    try:
+        with open(TRAFFIC_FILE) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        table = {}
+    table[workload] = out
+    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(table, f, indent=1, sort_keys=True)
+        f.write("\n")
+    return out
 
 
 def main():
@@ -106,7 +159,14 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run 5 plain device copies of one x buffer (reads and writes "
                          "B*S*D elements each) as the reference kernel for HBM counter scaling")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_RUN", "WRITE_RUN"),
+                    help="no GPU work: turn two rocprofv3 --pmc outputs (FETCH_SIZE, WRITE_SIZE) of "
+                         "'bench.py --calibrate-copy --workload W' into HBM bytes per launch for W, "
+                         "stored in profiles/hbm_traffic.json")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(json.dumps({args.workload: pmc_summary(*args.pmc_summary, args.workload)}, indent=1))
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; the hot path shards over batch/heads with no "
@@ -128,42 +188,59 @@ def main():
     outs = [torch.empty_like(x0) for _ in range(args.sets)]
     del inp
 
+    # EMA state: every launch reads ema_init and writes ema_final; chunks
+    # ping-pong between two state buffers.
+    state0 = torch.zeros(cfg.B, cfg.D, device=dev)
+    states = [torch.empty_like(state0), torch.empty_like(state0)]
+    grad = torch.empty(cfg.B, cfg.H, cfg.K, cfg.hd, device=dev) if cfg.ttt else None
+
     def step(i):
         x, out = xs[i % args.sets], outs[i % args.sets]
         if cfg.ttt:
-            cheby_ema_ttt(x, c, damp, lam, g=g, out=out)
+            cheby_ema_ttt(x, c, damp, lam, g=g, out=out, ema_init=state0, state_out=states[0], grad_out=grad)
         elif cfg.chunk:
-            state = None
-            for t0 in range(0, cfg.S, cfg.chunk):
-                _, state = cheby_ema_forward(x[:, t0:t0 + cfg.chunk], c, damp, lam, ema_init=state,
-                                             out=out[:, t0:t0 + cfg.chunk], return_state=True)
+            prev = state0
+            for n, t0 in enumerate(range(0, cfg.S, cfg.chunk)):
+                cheby_ema_forward(x[:, t0:t0 + cfg.chunk], c, damp, lam, ema_init=prev,
+                                  out=out[:, t0:t0 + cfg.chunk], state_out=states[n % 2])
+                prev = states[n % 2]
         else:
-            cheby_ema_forward(x, c, damp, lam, g=g, out=out)
+            cheby_ema_forward(x, c, damp, lam, g=g, out=out, ema_init=state0, state_out=states[0])
 
     stream = torch.cuda.current_stream(dev)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
 
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # Timed region: exactly K steps between two events on the launch stream,
+    # nothing else enqueued in between, so the average step is the average
+    # duration of the fused operator's launch(es) back to back.
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record(stream)
     for i in range(args.steps):
-        ev[i][0].record(stream)
         step(i)
-        ev[i][1].record(stream)
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
-    per = sorted(a.elapsed_time(b) for a, b in ev)
-    med = per[len(per) // 2]
-    mean_kernel_ms = sum(per) / len(per)
     ms_per_step = total_ms / args.steps
+    # Spread of single steps (a second, separately timed pass with an event
+    # pair around every step; each pair adds a few microseconds of dispatch
+    # overhead, so these read slightly high).
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        step(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) for a, b in ev)
     tokens = cfg.B * cfg.S
     algo = algorithmic_bytes(cfg)
-    achieved_gbs = algo / (mean_kernel_ms * 1e-3) / 1e9
+    launches = cfg.S // cfg.chunk if cfg.chunk else 1
+    mean_kernel_ms = ms_per_step / launches
+    algo_launch = algo / launches
+    achieved_gbs = algo_launch / (mean_kernel_ms * 1e-3) / 1e9
 
     res = {
         "metric": METRIC if args.workload == "headline" else f"Clenshaw+EMA tokens/s, workload {cfg.name}",
@@ -193,11 +270,12 @@ def main():
             "unit": "GB/s",
             "frac": achieved_gbs / HBM_PEAK_GBS,
             "traffic": measured_traffic(args.workload),
-            "algorithmic_bytes": algo,
+            "algorithmic_bytes": algo_launch,
+            "launches_per_step": launches,
             "kernel_ms_mean": mean_kernel_ms,
-            "kernel_ms_p10": per[len(per) // 10],
-            "kernel_ms_median": med,
-            "kernel_ms_p90": per[(9 * len(per)) // 10],
+            "step_ms_evented_p10": per[len(per) // 10],
+            "step_ms_evented_median": per[len(per) // 2],
+            "step_ms_evented_p90": per[(9 * len(per)) // 10],
         },
     }
     if args.calibrate_copy:

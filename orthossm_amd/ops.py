@@ -111,20 +111,20 @@ def cheby_ema_forward(x: torch.Tensor, coeffs: torch.Tensor, damping: Sequence[f
                       lam_shift: float = 0.004, lam_min: float = 0.9, lam_max: float = 0.9999,
                       ema_init: torch.Tensor | None = None, clamp: bool = True,
                       out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
-                      return_state: bool = False):
+                      return_state: bool = False, state_out: torch.Tensor | None = None):
     """Fused softsign -> Clenshaw -> damping -> tanh -> EMA on the GPU.
 
     x [B,S,D] fp32|bf16, coeffs [B,H,K,hd] fp32, damping/lam [H], g optional
     [S,H] or [B,S,H] (dynamic lambda), ema_init optional [B,D].
     Returns out [B,S,D] (dtype of x unless out_dtype), and ema_final [B,D]
-    fp32 when return_state.
+    fp32 when return_state.  ``state_out`` (contiguous [B,D] fp32 on the
+    device) receives ema_final instead of a new tensor.
     """
     lib = nat.load()
     a, out, keep = _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, clamp,
                             out_dtype, out)
     dev = out.device
-    ema_final = torch.empty((a.B, a.H * a.hd), device=dev, dtype=torch.float32) if return_state else None
-    a.ema_final = ema_final.data_ptr() if ema_final is not None else None
+    ema_final = _state_buffer(a, dev, return_state, state_out)
     stream = torch.cuda.current_stream(dev).cuda_stream
     nbytes = lib.osm_workspace_bytes(ctypes.byref(a), 0)
     if nbytes == 0:
@@ -140,10 +140,13 @@ def cheby_ema_ttt(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, *, g: tor
                   lam_shift: float = 0.004, lam_min: float = 0.9, lam_max: float = 0.9999,
                   ema_init: torch.Tensor | None = None, target: str = "x", clamp: bool = True,
                   out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
-                  return_state: bool = False):
+                  return_state: bool = False, state_out: torch.Tensor | None = None,
+                  grad_out: torch.Tensor | None = None):
     """Fused forward plus the TTT coefficient gradient
     grad[b,h,k,j] = d/dc MSE(out[:, :-1], y[:, 1:]) / (k+1)^2, y = x ('x') or
-    softsign(x) ('softsign').  Returns (out, grad) or (out, grad, ema_final)."""
+    softsign(x) ('softsign').  Returns (out, grad) or (out, grad, ema_final).
+    ``grad_out`` (contiguous [B,H,K,hd] fp32) and ``state_out`` receive the
+    results instead of new tensors."""
     lib = nat.load()
     tgt = {"x": nat.TARGET_X, "softsign": nat.TARGET_SOFTSIGN}.get(target)
     if tgt is None:
@@ -151,9 +154,12 @@ def cheby_ema_ttt(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, *, g: tor
     a, out, keep = _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, clamp,
                             out_dtype, out)
     dev = out.device
-    grad = torch.empty((a.B, a.H, a.K, a.hd), device=dev, dtype=torch.float32)
-    ema_final = torch.empty((a.B, a.H * a.hd), device=dev, dtype=torch.float32) if return_state else None
-    a.ema_final = ema_final.data_ptr() if ema_final is not None else None
+    if grad_out is None:
+        grad = torch.empty((a.B, a.H, a.K, a.hd), device=dev, dtype=torch.float32)
+    else:
+        _check_dest(grad_out, (a.B, a.H, a.K, a.hd), dev, "grad_out")
+        grad = grad_out
+    ema_final = _state_buffer(a, dev, return_state, state_out)
     stream = torch.cuda.current_stream(dev).cuda_stream
     nbytes = lib.osm_workspace_bytes(ctypes.byref(a), 1)
     if nbytes == 0:
@@ -163,6 +169,25 @@ def cheby_ema_ttt(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, *, g: tor
                                     ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(stream)))
     del keep
     return (out, grad, ema_final) if return_state else (out, grad)
+
+
+def _check_dest(t: torch.Tensor, shape, dev, name: str) -> None:
+    if t.dtype != torch.float32 or tuple(t.shape) != tuple(shape) or t.device != dev or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float32 tensor of shape {tuple(shape)} on {dev}")
+
+
+def _state_buffer(a, dev, return_state: bool, state_out: torch.Tensor | None):
+    """ema_final destination: state_out if given, a new [B,D] tensor if
+    return_state, else none (the kernel then skips the store)."""
+    if state_out is not None:
+        _check_dest(state_out, (a.B, a.H * a.hd), dev, "state_out")
+        buf = state_out
+    elif return_state:
+        buf = torch.empty((a.B, a.H * a.hd), device=dev, dtype=torch.float32)
+    else:
+        buf = None
+    a.ema_final = buf.data_ptr() if buf is not None else None
+    return buf
 
 
 def _rc_from_error(lib, a, ttt: int) -> int:
