@@ -1,0 +1,33 @@
+"""Host-side behaviour of the drop-in apply_cheby_rkv_v10 that needs no GPU:
+the paths it does not implement raise instead of changing semantics."""
+import pytest
+import torch
+
+from orthossm_amd import apply_cheby_rkv_core, apply_cheby_rkv_v10
+
+
+def test_alias():
+    assert apply_cheby_rkv_core is apply_cheby_rkv_v10
+
+
+def test_full_path_raises():
+    x = torch.zeros(1, 512, 64)
+    c = torch.zeros(1, 4, 4, 16)
+    with pytest.raises(NotImplementedError):
+        apply_cheby_rkv_v10(x, c, None, n_heads=4, seq_threshold=384)
+    with pytest.raises(NotImplementedError):
+        apply_cheby_rkv_v10(x, c, None, n_heads=4, seq_threshold=0)
+
+
+def test_gradients_raise():
+    x = torch.zeros(1, 16, 64, requires_grad=True)
+    c = torch.zeros(1, 4, 4, 16)
+    with pytest.raises(NotImplementedError):
+        apply_cheby_rkv_v10(x, c, None, n_heads=4)
+
+
+def test_cpu_tensor_raises():
+    x = torch.zeros(1, 16, 64)
+    c = torch.zeros(1, 4, 4, 16)
+    with pytest.raises(RuntimeError, match="ROCm GPU only"):
+        apply_cheby_rkv_v10(x, c, None, n_heads=4)

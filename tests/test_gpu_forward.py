@@ -198,3 +198,22 @@ def test_dynamic_config_full_size(dev):
         want, wfin = oracle_forward(sub)
         assert_close_fp32(out[b:b + 1], want)
         assert_close_fp32(fin[b:b + 1], wfin, what="ema_final")
+
+
+def test_drop_in_fast_path_matches_oracle(dev):
+    """apply_cheby_rkv_v10 on the fixed-coefficient path (S < seq_threshold):
+    V10 damping 0.98 - 0.06h/H and one scalar momentum for every head
+    (sdpc_kernel.py:1708-1744); coefficients and momentum come back as given."""
+    from orthossm_amd import apply_cheby_rkv_v10
+
+    H, hd, S = 4, 32, 300
+    inp = inputs(2, S, H, hd, K=4, seed=7)
+    x, c = inp["x"].to(dev), inp["coeffs"].to(dev)
+    mom = torch.randn_like(c)
+    out, c2, m2 = apply_cheby_rkv_v10(x, c, mom, n_heads=H, ema_momentum=0.9, seq_threshold=384)
+    torch.cuda.synchronize()
+    damping = 0.98 - 0.06 * np.arange(H) / H
+    want, _ = O.forward(inp["x"].double().numpy(), inp["coeffs"].numpy(), damping, np.full(H, 0.9))
+    assert out.dtype == torch.float32
+    assert_close_fp32(out.cpu(), want)
+    assert c2.data_ptr() == c.data_ptr() and m2.data_ptr() == mom.data_ptr()
