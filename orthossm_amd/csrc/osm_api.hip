@@ -80,7 +80,7 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
       return fail(OSM_E_LAYOUT, "out rows/batches overlap (out_stride_s=%lld < D or out_stride_b too small)",
                   (long long)a->out_stride_s);
     // One tile's byte span must fit a buffer descriptor's 31-bit offsets.
-    const int64_t tile_rows = std::max<int64_t>(osm::kMaxFwdTile, osm::TttGeo::TILE);
+    const int64_t tile_rows = std::max<int64_t>(osm::kMaxFwdTile, osm::TttTile::TILE) + 1;
     if ((tile_rows * a->x_stride_s + D) * xs >= (int64_t(1) << 31) ||
         (tile_rows * a->out_stride_s + D) * os >= (int64_t(1) << 31))
       return fail(OSM_E_LAYOUT, "token stride too large for 31-bit tile offsets");
@@ -96,7 +96,7 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
   }
   const int64_t n_lbd = (D + 63) / 64;
   const int64_t n_lb = a->B * n_lbd;
-  const int64_t tile = ttt ? osm::TttGeo::TILE : osm::fwd_tile_tokens(geo->dyn, n_lb, a->S);
+  const int64_t tile = ttt ? osm::ttt_tile_tokens(geo->dyn, a->x_dtype) : osm::fwd_tile_tokens(geo->dyn, n_lb, a->S);
   const int64_t n_tiles = (a->S + tile - 1) / tile;
   const int64_t n_lb_pad = (n_lb + 7) / 8 * 8;
   if (n_lb_pad * n_tiles >= (int64_t(1) << 31) || a->S >= (int64_t(1) << 31) - tile)
@@ -285,7 +285,7 @@ int osm_cheby_ema_ttt(const osm_cheby_args* args, float* grad, int target, void*
   p.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((slot_bytes + 255) / 256) * 256);
   p.ttt_scale = args->S > 1 ? (float)(2.0 / ((double)args->B * (double)(args->S - 1) * (double)p.D)) : 0.0f;
   p.ttt_target = target;
-  const hipError_t e = osm::launch_ttt(p, grad, args->x_dtype, args->out_dtype, geo.dyn, geo.kpad, st);
+  const hipError_t e = osm::launch_ttt(p, grad, args->x_dtype, args->out_dtype, geo.dyn, geo.tile, geo.kpad, st);
   if (e != hipSuccess) return hip_fail(e, "TTT kernel launch");
   return ok();
 }

@@ -16,7 +16,7 @@
 //   5. pass 2: replay s = lam*s + w from the carry, store out.
 // All tensor traffic uses buffer descriptors (osm_device.h): no per-element
 // address arithmetic and no bounds branches.
-#include "osm_chain.h"
+#include "osm_tile.h"
 
 namespace osm {
 namespace {
@@ -28,53 +28,6 @@ __device__ __forceinline__ float ema_input_exact(float x, const float (&a)[KP], 
   const float r = tanh_r(horner<KP>(softsign(x), a));
   const float w = __builtin_fmaf(neg2_one_m, r, one_m);
   return (x == x) ? w : 0.0f;
-}
-
-// Descriptors of one tile and this thread's offsets into them.
-struct TileAddr {
-  Rsrc x, out, g, c;
-  uint32_t vx, vo, vg;       // per-thread byte offsets (kOffOOB: lanes >= D)
-  uint32_t sx, so, sg, sc;   // uniform byte steps: one token (x, out, g), one k (coeffs)
-  int h;
-};
-
-template <class G, bool DYN, typename XT, typename OT>
-__device__ __forceinline__ TileAddr tile_addr(const FwdParams& p, const ThreadPos& q, const TileInfo& ti) {
-  TileAddr a;
-  const int t_tile = ti.tile * G::TILE;
-  const int d0 = ti.lbd * kLanes + q.lt * G::LPT;
-  const bool lane_ok = d0 < p.D;
-  const uint64_t rows_after = (uint64_t)(p.S - 1 - t_tile);
-  a.h = lane_ok ? d0 / p.hd : 0;
-  const int64_t row0 = (int64_t)q.tg * G::R;
-  // x and out: the extent ends after row S-1, so padding rows read 0 and
-  // their stores are dropped.
-  const char* xb = static_cast<const char*>(p.x) + ((int64_t)ti.b * p.x_sb + (int64_t)t_tile * p.x_ss) * sizeof(XT);
-  a.x = make_rsrc(xb, (rows_after * p.x_ss + p.D) * sizeof(XT));
-  a.sx = (uint32_t)(p.x_ss * sizeof(XT));
-  a.vx = lane_ok ? (uint32_t)((row0 * p.x_ss + d0) * sizeof(XT)) : kOffOOB;
-  char* ob = static_cast<char*>(p.out) + ((int64_t)ti.b * p.o_sb + (int64_t)t_tile * p.o_ss) * sizeof(OT);
-  a.out = make_rsrc(ob, (rows_after * p.o_ss + p.D) * sizeof(OT));
-  a.so = (uint32_t)(p.o_ss * sizeof(OT));
-  a.vo = lane_ok ? (uint32_t)((row0 * p.o_ss + d0) * sizeof(OT)) : kOffOOB;
-  if constexpr (DYN) {
-    const char* gb = reinterpret_cast<const char*>(p.g) + ((int64_t)ti.b * p.g_sb + (int64_t)t_tile * p.g_ss) * 4;
-    a.g = make_rsrc(gb, (rows_after * p.g_ss + (uint64_t)(p.H - 1) * p.g_sh + 1) * 4);
-    a.sg = (uint32_t)(p.g_ss * 4);
-    a.vg = (uint32_t)((row0 * p.g_ss + (int64_t)a.h * p.g_sh) * 4);
-  }
-  const char* cb = reinterpret_cast<const char*>(p.coeffs) + (int64_t)ti.b * p.c_sb * 4;
-  a.c = make_rsrc(cb, kMaxExtent);
-  a.sc = (uint32_t)(p.c_sk * 4);
-  return a;
-}
-
-// Advances a uniform byte offset by `step` in a way the compiler cannot fold:
-// otherwise every r * step product is materialised in its own SGPR.
-__device__ __forceinline__ uint32_t next_off(uint32_t off, uint32_t step) {
-  off += step;
-  asm volatile("" : "+s"(off));
-  return off;
 }
 
 // Rare path: a run whose aggregate is NaN saw a NaN or infinite input (or
@@ -143,30 +96,10 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   }
   const TileAddr a = tile_addr<G, DYN, XT, OT>(p, q, ti);
 
-  // Monomial coefficients of the series for the tile's 64 lanes, scaled by
-  // 2*log2(e)*damping (the tanh argument in exp2 units): wave j < KP forms
-  // coefficient j of every lane from <= 4 Chebyshev coefficients in float64
-  // and shares it through LDS.  Its loads are issued before those of x so
-  // that the conversion only waits for them.
-  static_assert(KP <= G::WAVES && KP <= 8, "one wave per monomial coefficient");
+  // Monomial coefficients (loads first, converted after the x loads).
+  static_assert(KP <= G::WAVES, "one wave per monomial coefficient");
   __shared__ float mono[KP][kLanes];
-  const int jw = __builtin_amdgcn_readfirstlane(q.wave);
-  float cm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  float kap_l = 0.0f;
-  if (jw < KP) {
-    const int d = ti.lbd * kLanes + q.wl;
-    const bool ok = d < p.D;
-    const int h = ok ? d / p.hd : 0;
-    const uint32_t vc = ok ? (uint32_t)(((int64_t)h * p.c_sh + (d - h * p.hd)) * 4) : kOffOOB;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int k = jw + 2 * i;
-      float v[1];
-      BufVec<float, 1>::load(a.c, k < p.K ? vc : kOffOOB, (uint32_t)k * a.sc, v);
-      cm[i] = v[0];
-    }
-    kap_l = kTwoLog2e * p.damping[h];
-  }
+  const MonoLoad ml = mono_issue<KP>(p, q, ti, a);
 
   // x rows of this thread's run, g (dynamic lambda).
   float w[R][LPT];
@@ -191,18 +124,10 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     }
   }
 
-  if (jw < KP) {
-    double acc = 0.0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc = __builtin_fma((double)kChebMono[jw][i], (double)cm[i], acc);
-    mono[jw][q.wl] = (float)(acc * (double)kap_l);
-  }
+  mono_store<KP>(ml, q, mono);
   __syncthreads();
   float c[LPT][KP];
-#pragma unroll
-  for (int j = 0; j < KP; ++j)
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) c[i][j] = mono[j][q.lt * LPT + i];
+  mono_read<G, KP>(mono, q, c);
 
   // Pass 1: w = (1 - lam) * tanh(damping * p(u)) in place of x, and the run
   // aggregate (A, B) from a zero state.  softsign as copysign(1 - 1/(1+|x|), x):
@@ -232,8 +157,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
       lamv[r0 + rr] = lam;
 #pragma unroll
       for (int i = 0; i < LPT; ++i) {
-        const float x = w[r0 + rr][i];
-        u[rr][i] = __builtin_copysignf(1.0f - __builtin_amdgcn_rcpf(1.0f + __builtin_fabsf(x)), x);
+        u[rr][i] = softsign_fast(w[r0 + rr][i]);
         py[rr][i] = c[i][KP - 1];
       }
     }

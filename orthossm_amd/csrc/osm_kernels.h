@@ -41,8 +41,10 @@ using FwdTileSmall = TileGeo<2, 8, 8>;     // 128 tokens
 constexpr int kMaxFwdTile = FwdTileLarge::TILE;
 // Tokens per forward tile for a launch with n_lb lane-blocks over S tokens.
 int fwd_tile_tokens(bool dyn, int64_t n_lb, int64_t S);
-// TTT: keeps x, r and dL/ds per token in registers -> shorter runs.
-using TttGeo = TileGeo<2, 8, 8>;
+// TTT: keeps the raw x and r = 1/(1+exp(2 damping p)) of every token of the
+// run in registers, plus 2K gradient accumulators per lane: 8-token runs.
+using TttTile = TileGeo<2, 8, 8>;   // 128 tokens
+int ttt_tile_tokens(bool dyn, int x_dtype);
 
 // Workspace: a kHeaderBytes header (launch epoch, fault word, completion
 // counters), then the look-back words, then (TTT only) per-tile partials.
@@ -82,7 +84,7 @@ size_t ttt_workspace_bytes(int n_lb, int n_tiles, bool dyn, int K);
 // Launchers: return hipSuccess or the launch error.
 hipError_t launch_fwd(const FwdParams& p, int x_dtype, int out_dtype, bool dyn, int tile, int kpad,
                       hipStream_t stream);
-hipError_t launch_ttt(const FwdParams& p, float* grad, int x_dtype, int out_dtype, bool dyn,
+hipError_t launch_ttt(const FwdParams& p, float* grad, int x_dtype, int out_dtype, bool dyn, int tile,
                       int kpad, hipStream_t stream);
 hipError_t launch_fill_zero(void* ptr, size_t bytes, hipStream_t stream);
 hipError_t launch_copy_state(const float* src, float* dst, size_t n, hipStream_t stream);

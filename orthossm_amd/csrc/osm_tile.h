@@ -1,0 +1,122 @@
+// Per-tile addressing and coefficient set-up shared by the forward and TTT
+// kernels: buffer descriptors rebased on the tile, the thread's lane offsets,
+// and the monomial form of each lane's Chebyshev series.
+#pragma once
+
+#include "osm_chain.h"
+
+namespace osm {
+
+// Descriptors of one tile and this thread's offsets into them.
+struct TileAddr {
+  Rsrc x, out, g, c;
+  uint32_t vx, vo, vg;       // per-thread byte offsets (kOffOOB: lanes >= D)
+  uint32_t sx, so, sg, sc;   // uniform byte steps: one token (x, out, g), one k (coeffs)
+  int h;                     // head of the thread's lanes
+};
+
+// x, out (and g) descriptors start at the tile's first row and end after row
+// S-1: rows past the sequence read 0 and their stores are dropped, and rows
+// after the tile (still < S) can be read through the same descriptor.
+template <class G, bool DYN, typename XT, typename OT>
+__device__ __forceinline__ TileAddr tile_addr(const FwdParams& p, const ThreadPos& q, const TileInfo& ti) {
+  TileAddr a;
+  const int t_tile = ti.tile * G::TILE;
+  const int d0 = ti.lbd * kLanes + q.lt * G::LPT;
+  const bool lane_ok = d0 < p.D;
+  const uint64_t rows_after = (uint64_t)(p.S - 1 - t_tile);
+  a.h = lane_ok ? d0 / p.hd : 0;
+  const int64_t row0 = (int64_t)q.tg * G::R;
+  const char* xb = static_cast<const char*>(p.x) + ((int64_t)ti.b * p.x_sb + (int64_t)t_tile * p.x_ss) * sizeof(XT);
+  a.x = make_rsrc(xb, (rows_after * p.x_ss + p.D) * sizeof(XT));
+  a.sx = (uint32_t)(p.x_ss * sizeof(XT));
+  a.vx = lane_ok ? (uint32_t)((row0 * p.x_ss + d0) * sizeof(XT)) : kOffOOB;
+  char* ob = static_cast<char*>(p.out) + ((int64_t)ti.b * p.o_sb + (int64_t)t_tile * p.o_ss) * sizeof(OT);
+  a.out = make_rsrc(ob, (rows_after * p.o_ss + p.D) * sizeof(OT));
+  a.so = (uint32_t)(p.o_ss * sizeof(OT));
+  a.vo = lane_ok ? (uint32_t)((row0 * p.o_ss + d0) * sizeof(OT)) : kOffOOB;
+  if constexpr (DYN) {
+    const char* gb = reinterpret_cast<const char*>(p.g) + ((int64_t)ti.b * p.g_sb + (int64_t)t_tile * p.g_ss) * 4;
+    a.g = make_rsrc(gb, (rows_after * p.g_ss + (uint64_t)(p.H - 1) * p.g_sh + 1) * 4);
+    a.sg = (uint32_t)(p.g_ss * 4);
+    a.vg = (uint32_t)((row0 * p.g_ss + (int64_t)a.h * p.g_sh) * 4);
+  }
+  const char* cb = reinterpret_cast<const char*>(p.coeffs) + (int64_t)ti.b * p.c_sb * 4;
+  a.c = make_rsrc(cb, kMaxExtent);
+  a.sc = (uint32_t)(p.c_sk * 4);
+  return a;
+}
+
+// Advances a uniform byte offset by `step` in a way the compiler cannot fold:
+// otherwise every r * step product is materialised in its own SGPR.
+__device__ __forceinline__ uint32_t next_off(uint32_t off, uint32_t step) {
+  off += step;
+  asm volatile("" : "+s"(off));
+  return off;
+}
+
+// Monomial coefficients of the series for the tile's 64 lanes, scaled by
+// 2*log2(e)*damping (the tanh argument in exp2 units).  Wave j < KP forms
+// coefficient j of every lane from <= 4 Chebyshev coefficients (kChebMono)
+// in float64 and shares it through LDS.  Split in three steps so the caller
+// can issue these loads before its bulk loads (the conversion then waits only
+// for them) and convert after issuing those:
+//   MonoLoad m = mono_issue(...);  <bulk loads>;  mono_store(m, ...);
+//   __syncthreads();  mono_read(...)
+struct MonoLoad {
+  float cm[4];
+  float kap;
+  int j;   // coefficient of this wave (wave-uniform); >= KP: none
+};
+
+template <int KP>
+__device__ __forceinline__ MonoLoad mono_issue(const FwdParams& p, const ThreadPos& q, const TileInfo& ti,
+                                               const TileAddr& a) {
+  MonoLoad m;
+  m.j = __builtin_amdgcn_readfirstlane(q.wave);
+  m.kap = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m.cm[i] = 0.0f;
+  if (m.j < KP) {
+    const int d = ti.lbd * kLanes + q.wl;
+    const bool ok = d < p.D;
+    const int h = ok ? d / p.hd : 0;
+    const uint32_t vc = ok ? (uint32_t)(((int64_t)h * p.c_sh + (d - h * p.hd)) * 4) : kOffOOB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = m.j + 2 * i;
+      float v[1];
+      BufVec<float, 1>::load(a.c, k < p.K ? vc : kOffOOB, (uint32_t)k * a.sc, v);
+      m.cm[i] = v[0];
+    }
+    m.kap = kTwoLog2e * p.damping[h];
+  }
+  return m;
+}
+
+template <int KP>
+__device__ __forceinline__ void mono_store(const MonoLoad& m, const ThreadPos& q, float (&mono)[KP][kLanes]) {
+  if (m.j < KP) {
+    double acc = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = __builtin_fma((double)kChebMono[m.j][i], (double)m.cm[i], acc);
+    mono[m.j][q.wl] = (float)(acc * (double)m.kap);
+  }
+}
+
+template <class G, int KP>
+__device__ __forceinline__ void mono_read(const float (&mono)[KP][kLanes], const ThreadPos& q,
+                                          float (&c)[G::LPT][KP]) {
+#pragma unroll
+  for (int j = 0; j < KP; ++j)
+#pragma unroll
+    for (int i = 0; i < G::LPT; ++i) c[i][j] = mono[j][q.lt * G::LPT + i];
+}
+
+// Fast softsign copysign(1 - 1/(1 + |x|), x): +-Inf and huge |x| give +-1
+// (the reciprocal underflows to 0); absolute error ~6e-8; NaN stays NaN.
+__device__ __forceinline__ float softsign_fast(float x) {
+  return __builtin_copysignf(1.0f - __builtin_amdgcn_rcpf(1.0f + __builtin_fabsf(x)), x);
+}
+
+}  // namespace osm

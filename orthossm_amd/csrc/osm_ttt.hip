@@ -1,54 +1,190 @@
 // Fused Cheby-RKV forward + TTT coefficient gradient for gfx950.
 //
 // Loss L = mean_{b, t<S-1, d} (out[t] - y[t+1])^2 (y = x or softsign(x)).
-// Its adjoint is a reverse recurrence
-//     gL[t] = 2/N (out[t] - y[t+1]) * [-1 <= s[t] <= 1],   t < S-1 (0 at S-1)
-//     a[t]  = gL[t] + lam[t+1] a[t+1]
-//     dL/dc_k = sum_t a[t] D[t] T_k(u[t]),  D = (1-lam) * damping * (1 - z^2)
+// With e[t] = out[t] - y[t+1] (0 at t = S-1, and where the output clamp
+// binds) the adjoint of the state is the reverse recurrence
+//     a[t] = (2/N) e[t] + lam[t+1] a[t+1]
+// and dL/dc_k = sum_t a[t] D[t] T_k(u[t]),  D = (1-lam) damping (1 - z^2)
 // (reference chain: _parallel_reverse_ema_kernel, sdpc_kernel.py:681-777;
 // _parallel_backward_clenshaw_kernel_v10, sdpc_kernel.py:784-915; the
 // per-tile partial sum, sdpc_kernel.py:2502).
 //
 // One pass over HBM: each tile runs the forward of osm_fwd.hip (x read once,
-// out written once), then sweeps its tokens backwards.  a[t] inside a tile is
-// a[t] = at[t] + Lam[t] * rho, where at is the tile-local reverse scan from
-// zero, Lam[t] the decay product to the tile end and rho the (unknown)
-// reverse carry from later tiles.  The tile therefore emits
-//     P_k = sum_t at[t] D[t] T_k(u[t]),   Q_k = sum_t Lam[t] D[t] T_k(u[t])
-// and its reverse map rho_prev = Ar * rho + Br.  Two small kernels merge the
-// tiles of each lane from the end of the sequence (rho = 0 there) in a fixed
-// order: G_k = sum_tiles (P_k + rho_tile Q_k), scaled by 1/(k+1)^2.
-#include "osm_chain.h"
+// out written once) and accumulates the gradient in the same forward sweep.
+// Swapping the order of summation turns the reverse adjoint into forward
+// accumulators: for a run of tokens t0..T, followed by the adjoint rho =
+// a[T+1] from later tokens,
+//     sum_t a[t] v[t] = sum_t e[t] F[t] + lam[T+1] F[T] rho,
+//     F[t] = lam[t] F[t-1] + v[t]            (F[t0-1] = 0),
+// with v = D T_k(u) for each k.  So a run yields P_k = sum_t e[t] F_k[t], the
+// end values F_k[T], and its adjoint map a[t0] = alpha + beta rho.  Runs are
+// composed in LDS into the tile's (P, Q) and map; two small kernels merge the
+// tiles of each lane from the end of the sequence (rho = 0) in a fixed order:
+// G_k = sum_tiles (P_k + Q_k rho_tile), scaled by 1/(k+1)^2.
+#include "osm_tile.h"
 
 namespace osm {
 namespace {
 
-using G = TttGeo;
 constexpr int kChunk = 16;  // tiles merged per thread by the first merge kernel
 
 template <int KP>
 __host__ __device__ constexpr int n_fields() {
-  return 2 * KP + 2;  // P_0..P_{KP-1}, Q_0..Q_{KP-1}, Ar, Br
+  return 2 * KP + 2;  // P_0..P_{KP-1}, Q_0..Q_{KP-1}, Ar (beta), Br (alpha)
 }
 
-// Sum over the token groups of a wave (lanes wl, wl^TPR, ...).
+// One row of a thread's LPT = 2 lanes of x, kept raw between the passes
+// (bf16: both lanes in one register).  opaque() hides the value from the
+// compiler so that pass 2 re-derives u from it instead of keeping pass 1's
+// unpacked x and u alive across the look-back (twice the registers).
+template <typename XT>
+struct XRow;
+
+template <>
+struct XRow<float> {
+  float v[2];
+  __device__ __forceinline__ void zero() { v[0] = v[1] = 0.0f; }
+  __device__ __forceinline__ void load(Rsrc r, uint32_t vo, uint32_t so) { BufVec<float, 2>::load(r, vo, so, v); }
+  __device__ __forceinline__ float get(int i) const { return v[i]; }
+  __device__ __forceinline__ void opaque() { asm volatile("" : "+v"(v[0]), "+v"(v[1])); }
+};
+
+template <>
+struct XRow<__bf16> {
+  unsigned v;
+  __device__ __forceinline__ void zero() { v = 0u; }
+  __device__ __forceinline__ void load(Rsrc r, uint32_t vo, uint32_t so) {
+    v = __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, kNT);
+  }
+  __device__ __forceinline__ float get(int i) const { return __uint_as_float(i == 0 ? v << 16 : v & 0xffff0000u); }
+  __device__ __forceinline__ void opaque() { asm volatile("" : "+v"(v)); }
+};
+
+// Target y of one x value.
+template <bool SOFT>
+__device__ __forceinline__ float target_of(float x) {
+  if constexpr (SOFT) return (x == x) ? softsign(x) : x;
+  return x;
+}
+
+// Gradient state of one thread's run.
+template <int KP, int LPT>
+struct RunGrad {
+  float F[KP][LPT];   // forward-discounted basis sums
+  float P[KP][LPT];   // sum_t e[t] F[t]
+  float al[LPT];      // adjoint at the run start from this run's e (unscaled)
+  float Lp;           // prod of lam over (t0, t]
+};
+
+// Pass 2 over a thread's run, in token order: the EMA from the carried state
+// s, out = clamp(s), e[t] = out[t] - y[t+1], and the gradient accumulators.
+// SLOW handles, per element, NaN inputs (D = 0, u = 0), a binding clamp
+// (e = 0 where |s| > 1), the sequence end (e = 0 for t >= S-1) and the
+// ema_final capture; the fast variant assumes none of them occurs in the run.
+template <class G, bool DYN, bool SOFT, bool SLOW, typename XT, typename OT, int KP>
+__device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G::LPT], const XRow<XT> (&xr)[G::R],
+                                          const float (&rr)[G::R][G::LPT], const float (&lamv)[G::R],
+                                          const float (&y_after)[G::LPT], const TileAddr& a, float lo, float hi,
+                                          int t_first, int S, bool clamp, float* fin) {
+  constexpr int R = G::R, LPT = G::LPT;
+#pragma unroll
+  for (int k = 0; k < KP; ++k)
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) rg.F[k][i] = rg.P[k][i] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) rg.al[i] = 0.0f;
+  rg.Lp = 1.0f;
+  float u[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) u[i] = softsign_fast(xr[0].get(i));
+  uint32_t so = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float lam = lamv[r];
+    const float one_m = 1.0f - lam;
+    const float n2 = -2.0f * one_m;
+    if (r > 0) rg.Lp *= lam;
+    float un[LPT], yn[LPT];
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      if (r + 1 < R) {
+        const float xn = xr[r + 1].get(i);
+        un[i] = softsign_fast(xn);
+        yn[i] = SOFT ? ((xn == xn) ? un[i] : xn) : xn;
+      } else {
+        un[i] = 0.0f;
+        yn[i] = y_after[i];
+      }
+    }
+    float o[LPT];
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const float rv = rr[r][i];
+      s[i] = __builtin_fmaf(lam, s[i], __builtin_fmaf(n2, rv, one_m));
+      o[i] = __builtin_amdgcn_fmed3f(s[i], lo, hi);
+      float e = o[i] - yn[i];
+      float D = __builtin_fmaf(-rv, rv, rv);   // r (1 - r) = (1 - z^2) / 4
+      if constexpr (DYN) D *= one_m;
+      float uu = u[i];
+      if constexpr (SLOW) {
+        const int t = t_first + r;
+        const bool pass = !clamp || __builtin_fabsf(s[i]) <= 1.0f;
+        e = (t < S - 1 && pass) ? e : 0.0f;
+        const bool ok = xr[r].get(i) == xr[r].get(i);
+        D = ok ? D : 0.0f;
+        uu = ok ? uu : 0.0f;
+        if (fin && t == S - 1) fin[i] = s[i];
+      }
+      rg.al[i] = __builtin_fmaf(rg.Lp, e, rg.al[i]);
+      // v_k = D T_k(u) by the Chebyshev recurrence on the scaled values.
+      float vm2 = D, vm1 = D * uu;
+      const float u2 = uu + uu;
+      rg.F[0][i] = __builtin_fmaf(lam, rg.F[0][i], vm2);
+      rg.P[0][i] = __builtin_fmaf(e, rg.F[0][i], rg.P[0][i]);
+      if (KP > 1) {
+        rg.F[1][i] = __builtin_fmaf(lam, rg.F[1][i], vm1);
+        rg.P[1][i] = __builtin_fmaf(e, rg.F[1][i], rg.P[1][i]);
+      }
+#pragma unroll
+      for (int k = 2; k < KP; ++k) {
+        const float vk = __builtin_fmaf(u2, vm1, -vm2);
+        rg.F[k][i] = __builtin_fmaf(lam, rg.F[k][i], vk);
+        rg.P[k][i] = __builtin_fmaf(e, rg.F[k][i], rg.P[k][i]);
+        vm2 = vm1;
+        vm1 = vk;
+      }
+      u[i] = un[i];
+    }
+    BufVec<OT, LPT>::store(a.out, a.vo, so, o);
+    so = next_off(so, a.so);
+  }
+}
+
+// Sum over the token groups of a wave (lanes wl, wl ^ TPR, ...).
+template <class G>
 __device__ __forceinline__ float wave_sum_tg(float v) {
 #pragma unroll
   for (int m = G::TPR; m < 64; m *= 2) v += __shfl_xor(v, m);
   return v;
 }
 
-template <bool DYN, typename XT, typename OT, int KP>
-__global__ void __launch_bounds__(G::THREADS) cheby_ema_ttt_kernel(const FwdParams p) {
+// Two workgroups (4 waves per SIMD) per CU: at most 128 VGPRs.
+template <class G, bool DYN, bool SOFT, typename XT, typename OT, int KP>
+__global__ void __launch_bounds__(G::THREADS) __attribute__((amdgpu_waves_per_eu(4)))
+cheby_ema_ttt_kernel(const FwdParams p) {
   constexpr int R = G::R;
   constexpr int LPT = G::LPT;
   constexpr int NTG = G::NTG;
   constexpr int WORDS = DYN ? 2 : 1;
   constexpr int F = n_fields<KP>();
+  static_assert(LPT == 2, "XRow holds two lanes");
+  static_assert(KP <= G::WAVES, "one wave per monomial coefficient");
   __shared__ ChainLds<G> L;
-  __shared__ float sh_y0[NTG][kLanes];      // target y at each token group's first token
-  __shared__ float sh_rA[NTG][G::TPR];      // reverse map of each run
-  __shared__ float sh_rB[NTG][kLanes];
+  __shared__ float mono[KP][kLanes];
+  __shared__ float sh_y0[NTG][kLanes];      // target y at each run's first token
+  __shared__ float sh_lam0[NTG][G::TPR];    // lambda at each run's first token
+  __shared__ float sh_al[NTG][kLanes];      // run adjoint maps a[t0] = alpha + beta rho
+  __shared__ float sh_be[NTG][G::TPR];
   __shared__ float sh_red[G::WAVES][2 * KP][kLanes];
 
   const ThreadPos q = thread_pos<G>();
@@ -58,62 +194,49 @@ __global__ void __launch_bounds__(G::THREADS) cheby_ema_ttt_kernel(const FwdPara
     finish_block(p.hdr, tags.epoch);
     return;
   }
-  const int b = ti.b;
-  const int d0 = ti.lbd * kLanes + q.lt * LPT;
-  const bool lane_ok = d0 < p.D;
-  const int h = lane_ok ? d0 / p.hd : 0;
-  const int j0 = d0 - h * p.hd;
-  const int t0 = ti.tile * G::TILE + q.tg * R;
-  const bool soft_target = p.ttt_target == 1;
+  const TileAddr a = tile_addr<G, DYN, XT, OT>(p, q, ti);
+  const MonoLoad ml = mono_issue<KP>(p, q, ti, a);
 
-  const float delta = p.damping[h];
-  float c[LPT][KP];
+  // x rows of the run (raw), g (dynamic lambda), and for the tile's last run
+  // the row after the tile (its target y and lambda).
+  XRow<XT> xr[R];
   {
-    const float kap = kTwoLog2e * delta;
-    const float* cb = p.coeffs + (int64_t)b * p.c_sb + (int64_t)h * p.c_sh + j0;
-#pragma unroll
-    for (int k = 0; k < KP; ++k) {
-#pragma unroll
-      for (int i = 0; i < LPT; ++i)
-        c[i][k] = (lane_ok && k < p.K) ? kap * cb[(int64_t)k * p.c_sk + i] : 0.0f;
-    }
-  }
-  const float lam_h = p.lam[h];
-
-  const XT* xrow = reinterpret_cast<const XT*>(p.x) + (int64_t)b * p.x_sb + d0;
-  float xv[R][LPT];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int t = t0 + r;
-    if (lane_ok && t < p.S) {
-      LaneVec<XT, LPT>::load(xrow + (int64_t)t * p.x_ss, xv[r]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < LPT; ++i) xv[r][i] = 0.0f;
-    }
-  }
-  // Target of the token after the run: the next token group's first token
-  // (through LDS) or, for the last group, the next tile's first row.
-  float y_after[LPT];
-#pragma unroll
-  for (int i = 0; i < LPT; ++i) y_after[i] = 0.0f;
-  if (q.tg == NTG - 1 && lane_ok && t0 + R < p.S) LaneVec<XT, LPT>::load(xrow + (int64_t)(t0 + R) * p.x_ss, y_after);
-
-  float lamv[R];
-  {
-    const float* gp = DYN ? p.g + (int64_t)b * p.g_sb + (int64_t)h * p.g_sh : nullptr;
+    uint32_t so = 0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int t = t0 + r;
-      if (t < p.S) {
-        lamv[r] = DYN ? __builtin_amdgcn_fmed3f(__builtin_fmaf(p.lam_shift, gp[(int64_t)t * p.g_ss], lam_h),
-                                                p.lam_min, p.lam_max)
-                      : lam_h;
-      } else {
-        lamv[r] = 1.0f;
-      }
+      xr[r].load(a.x, a.vx, so);
+      so = next_off(so, a.sx);
     }
   }
+  const float lam_h = p.lam[a.h];
+  float lamv[R];
+  if constexpr (DYN) {
+    uint32_t sg = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float gv[1];
+      BufVec<float, 1>::load(a.g, a.vg, sg, gv);
+      lamv[r] = gv[0];
+      sg = next_off(sg, a.sg);
+    }
+  }
+  const bool last_run = q.tg == NTG - 1;
+  XRow<XT> x_after;
+  x_after.zero();
+  float g_after = 0.0f;
+  if (last_run) {
+    x_after.load(a.x, a.vx, (uint32_t)R * a.sx);
+    if constexpr (DYN) {
+      float gv[1];
+      BufVec<float, 1>::load(a.g, a.vg, (uint32_t)R * a.sg, gv);
+      g_after = gv[0];
+    }
+  }
+
+  mono_store<KP>(ml, q, mono);
+  __syncthreads();
+  float c[LPT][KP];
+  mono_read<G, KP>(mono, q, c);
 
   // Pass 1: r = 1/(1+exp(2 damping p)) per element and the run aggregate.
   float rr[R][LPT];
@@ -123,25 +246,41 @@ __global__ void __launch_bounds__(G::THREADS) cheby_ema_ttt_kernel(const FwdPara
   for (int i = 0; i < LPT; ++i) Bv[i] = 0.0f;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float lam = lamv[r];
+    float lam = lam_h;
+    if constexpr (DYN) lam = __builtin_amdgcn_fmed3f(__builtin_fmaf(p.lam_shift, lamv[r], lam_h), p.lam_min, p.lam_max);
+    lamv[r] = lam;
     const float one_m = 1.0f - lam;
     const float n2 = -2.0f * one_m;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const float x = xv[r][i];
-      rr[r][i] = tanh_r(clenshaw<KP>(softsign(x), c[i]));
-      const float w = (x == x) ? __builtin_fmaf(n2, rr[r][i], one_m) : 0.0f;
-      Bv[i] = __builtin_fmaf(lam, Bv[i], (t0 + r < p.S) ? w : 0.0f);
+      rr[r][i] = tanh_r(horner<KP>(softsign_fast(xr[r].get(i)), c[i]));
+      Bv[i] = __builtin_fmaf(lam, Bv[i], __builtin_fmaf(n2, rr[r][i], one_m));
     }
     A *= lam;
   }
-
-  // Targets at the first token of each run, for the neighbouring run.
+  bool bad = false;
 #pragma unroll
-  for (int i = 0; i < LPT; ++i) {
-    const float x = xv[0][i];
-    sh_y0[q.tg][q.lt * LPT + i] = (soft_target && x == x) ? softsign(x) : x;
+  for (int i = 0; i < LPT; ++i) bad |= Bv[i] != Bv[i];
+  if (bad) {
+    // A NaN input: z = 0 there (r = 1/2 gives w = 0); recompute the aggregate.
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) Bv[i] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float one_m = 1.0f - lamv[r];
+#pragma unroll
+      for (int i = 0; i < LPT; ++i) {
+        const float x = xr[r].get(i);
+        if (x != x) rr[r][i] = 0.5f;
+        Bv[i] = __builtin_fmaf(lamv[r], Bv[i], __builtin_fmaf(-2.0f * one_m, rr[r][i], one_m));
+      }
+    }
   }
+
+  // Target and lambda at each run's first token, for the preceding run.
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) sh_y0[q.tg][q.lt * LPT + i] = target_of<SOFT>(xr[0].get(i));
+  sh_lam0[q.tg][q.lt] = lamv[0];
 
   unsigned long long* lane_slots = p.slots + ((size_t)ti.lb * p.n_tiles * kLanes + q.wl) * WORDS;
   const size_t tile_stride = (size_t)kLanes * WORDS;
@@ -150,7 +289,7 @@ __global__ void __launch_bounds__(G::THREADS) cheby_ema_ttt_kernel(const FwdPara
 
   const int dl = ti.lbd * kLanes + q.wl;
   const bool dl_ok = dl < p.D;
-  const float init_wl = (p.ema_init && dl_ok) ? p.ema_init[(int64_t)b * p.D + dl] : 0.0f;
+  const float init_wl = (p.ema_init && dl_ok) ? p.ema_init[(int64_t)ti.b * p.D + dl] : 0.0f;
   const float lam_wl = DYN ? 0.0f : p.lam[dl_ok ? dl / p.hd : 0];
   {
     LookBack<G, DYN> lbk;
@@ -158,135 +297,79 @@ __global__ void __launch_bounds__(G::THREADS) cheby_ema_ttt_kernel(const FwdPara
     look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, lane_slots, tile_stride, init_wl, lam_wl, p.hdr);
   }
 
-  if (q.tg < NTG - 1) {
+  float y_after[LPT];
+  float lam_after;
+  if (!last_run) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) y_after[i] = sh_y0[q.tg + 1][q.lt * LPT + i];
-  } else if (soft_target) {
+    lam_after = sh_lam0[q.tg + 1][q.lt];
+  } else {
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) y_after[i] = (y_after[i] == y_after[i]) ? softsign(y_after[i]) : y_after[i];
+    for (int i = 0; i < LPT; ++i) y_after[i] = target_of<SOFT>(x_after.get(i));
+    lam_after = DYN ? __builtin_amdgcn_fmed3f(__builtin_fmaf(p.lam_shift, g_after, lam_h), p.lam_min, p.lam_max)
+                    : lam_h;
   }
 
-  // Pass 2 (forward): s from the carry, out, and the loss gradient gL.
-  float gl[R][LPT];
-  {
-    float s[LPT];
+  // Pass 2 from the carried state.
+  float s[LPT];
+  bool big = false;
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) s[i] = __builtin_fmaf(pA, L.carry[q.lt * LPT + i], pB[i]);
-    OT* orow = reinterpret_cast<OT*>(p.out) + (int64_t)b * p.o_sb + d0;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int t = t0 + r;
-      const float lam = lamv[r];
-      const float one_m = 1.0f - lam;
-      const float n2 = -2.0f * one_m;
-      float o[LPT];
-#pragma unroll
-      for (int i = 0; i < LPT; ++i) {
-        const float x = xv[r][i];
-        const float w = (x == x && t < p.S) ? __builtin_fmaf(n2, rr[r][i], one_m) : 0.0f;
-        s[i] = __builtin_fmaf(lam, s[i], w);
-        o[i] = p.clamp_out ? __builtin_amdgcn_fmed3f(s[i], -1.0f, 1.0f) : s[i];
-        float y;
-        if (r + 1 < R) {
-          const float xn = xv[r + 1][i];
-          y = (soft_target && xn == xn) ? softsign(xn) : xn;
-        } else {
-          y = y_after[i];
-        }
-        const bool pass = !p.clamp_out || (s[i] >= -1.0f && s[i] <= 1.0f);
-        gl[r][i] = (t < p.S - 1 && pass) ? p.ttt_scale * (o[i] - y) : 0.0f;
-      }
-      if (lane_ok && t < p.S) LaneVec<OT, LPT>::store(orow + (int64_t)t * p.o_ss, o);
-    }
-    if (ti.is_last && q.tg == NTG - 1 && lane_ok && p.ema_final) {
-#pragma unroll
-      for (int i = 0; i < LPT; ++i) p.ema_final[(int64_t)b * p.D + d0 + i] = s[i];
-    }
+  for (int i = 0; i < LPT; ++i) {
+    s[i] = __builtin_fmaf(pA, L.carry[q.lt * LPT + i], pB[i]);
+    big |= __builtin_fabsf(s[i]) > 1.0f;
   }
+  // |s| <= 1 at the run start keeps |s| <= 1 over the run (s is a convex
+  // combination of it and values of tanh), so the clamp can only bind if the
+  // carried state is already out of range.
+  const bool clamp = p.clamp_out != 0;
+  const float lo = clamp ? -1.0f : -__builtin_inff();
+  const float hi = clamp ? 1.0f : __builtin_inff();
+  const int t_first = ti.tile * G::TILE + q.tg * R;
+  float* fin = (ti.is_last && p.ema_final && a.vo != kOffOOB)
+                   ? p.ema_final + (int64_t)ti.b * p.D + ti.lbd * kLanes + q.lt * LPT
+                   : nullptr;
+  RunGrad<KP, LPT> rg;
+#pragma unroll
+  for (int r = 0; r < R; ++r) xr[r].opaque();
+  if (bad || (clamp && big) || ti.is_last)
+    ttt_pass2<G, DYN, SOFT, true, XT, OT, KP>(rg, s, xr, rr, lamv, y_after, a, lo, hi, t_first, p.S, clamp, fin);
+  else
+    ttt_pass2<G, DYN, SOFT, false, XT, OT, KP>(rg, s, xr, rr, lamv, y_after, a, lo, hi, t_first, p.S, clamp, fin);
 
-  // Reverse sweep over the run: at (local adjoint), Lam (decay to run end).
-  float P[KP][LPT], Q[KP][LPT];
+  // Compose the runs of the tile: rho of run g = Ar_g + Br_g rho_tile.
+  const float beta = rg.Lp * lam_after;
 #pragma unroll
-  for (int k = 0; k < KP; ++k)
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) P[k][i] = Q[k][i] = 0.0f;
-  float at[LPT];
-#pragma unroll
-  for (int i = 0; i < LPT; ++i) at[i] = 0.0f;
-  float Lam = 1.0f, lam_next = 1.0f;
-  const float dsc = 4.0f * delta;  // 1 - z^2 = 4 r (1 - r)
-#pragma unroll
-  for (int r = R - 1; r >= 0; --r) {
-    const int t = t0 + r;
-    const float lam = lamv[r];
-    Lam *= lam_next;
-    const float dl_scale = (t < p.S) ? (1.0f - lam) * dsc : 0.0f;
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const float x = xv[r][i];
-      const bool ok = x == x;
-      at[i] = __builtin_fmaf(lam_next, at[i], gl[r][i]);
-      const float rv = rr[r][i];
-      const float D = ok ? dl_scale * rv * (1.0f - rv) : 0.0f;
-      const float u = ok ? softsign(x) : 0.0f;
-      const float vp = at[i] * D;
-      const float vq = Lam * D;
-      const float u2 = u + u;
-      float Tm2 = 1.0f, Tm1 = u;
-      P[0][i] += vp;
-      Q[0][i] += vq;
-      if (KP > 1) {
-        P[1][i] = __builtin_fmaf(vp, u, P[1][i]);
-        Q[1][i] = __builtin_fmaf(vq, u, Q[1][i]);
-      }
-#pragma unroll
-      for (int k = 2; k < KP; ++k) {
-        const float Tk = __builtin_fmaf(u2, Tm1, -Tm2);
-        P[k][i] = __builtin_fmaf(vp, Tk, P[k][i]);
-        Q[k][i] = __builtin_fmaf(vq, Tk, Q[k][i]);
-        Tm2 = Tm1;
-        Tm1 = Tk;
-      }
-    }
-    lam_next = lam;
-  }
-  // Run reverse map: rho_prev = lam[t0] * (at[t0] + Lam[t0] * rho_run).
-  const float rA = lam_next * Lam;
-  float rB[LPT];
-#pragma unroll
-  for (int i = 0; i < LPT; ++i) rB[i] = lam_next * at[i];
-  sh_rA[q.tg][q.lt] = rA;
-#pragma unroll
-  for (int i = 0; i < LPT; ++i) sh_rB[q.tg][q.lt * LPT + i] = rB[i];
+  for (int i = 0; i < LPT; ++i) sh_al[q.tg][q.lt * LPT + i] = rg.al[i];
+  sh_be[q.tg][q.lt] = beta;
   __syncthreads();
-
-  // rho_run(tg) = alpha + beta * rho_tile, from the later runs in fixed order.
-  float alpha[LPT];
+  float Ar[LPT], Br = 1.0f;
 #pragma unroll
-  for (int i = 0; i < LPT; ++i) alpha[i] = 0.0f;
-  float beta = 1.0f;
+  for (int i = 0; i < LPT; ++i) Ar[i] = 0.0f;
   for (int g = NTG - 1; g > q.tg; --g) {
-    const float a = sh_rA[g][q.lt];
+    const float bg = sh_be[g][q.lt];
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) alpha[i] = __builtin_fmaf(a, alpha[i], sh_rB[g][q.lt * LPT + i]);
-    beta *= a;
+    for (int i = 0; i < LPT; ++i) Ar[i] = __builtin_fmaf(bg, Ar[i], sh_al[g][q.lt * LPT + i]);
+    Br *= bg;
   }
+  // Per-lane scale: 2/N and the constant part of D = 4 damping (1-lam) r(1-r).
+  const float ks = p.ttt_scale * 4.0f * p.damping[a.h] * (DYN ? 1.0f : 1.0f - lam_h);
   float* part = p.partials + ((size_t)ti.lb * p.n_tiles + ti.tile) * F * kLanes;
   if (q.tg == 0) {
-    // Tile reverse map: rho_prev_tile = rA*(alpha + beta*rho_tile) + rB.
+    // Tile map: a[tile start] = al_0 + beta_0 (Ar_0 + Br_0 rho_tile).
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      part[(size_t)(2 * KP) * kLanes + q.lt * LPT + i] = rA * beta;
-      part[(size_t)(2 * KP + 1) * kLanes + q.lt * LPT + i] = __builtin_fmaf(rA, alpha[i], rB[i]);
+      part[(size_t)(2 * KP) * kLanes + q.lt * LPT + i] = beta * Br;
+      part[(size_t)(2 * KP + 1) * kLanes + q.lt * LPT + i] = __builtin_fmaf(beta, Ar[i], rg.al[i]);
     }
   }
-  // Tile partials: P' = sum_runs (P + alpha Q), Q' = sum_runs beta Q.
+  // Run contributions P + lam_after F (Ar + Br rho_tile), summed over runs.
+  const float cB = lam_after * Br * ks;
 #pragma unroll
   for (int k = 0; k < KP; ++k) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const float pv = wave_sum_tg(__builtin_fmaf(alpha[i], Q[k][i], P[k][i]));
-      const float qv = wave_sum_tg(beta * Q[k][i]);
+      const float pv = wave_sum_tg<G>(ks * __builtin_fmaf(lam_after * Ar[i], rg.F[k][i], rg.P[k][i]));
+      const float qv = wave_sum_tg<G>(cB * rg.F[k][i]);
       if (q.wl < G::TPR) {
         sh_red[q.wave][k][q.lt * LPT + i] = pv;
         sh_red[q.wave][KP + k][q.lt * LPT + i] = qv;
@@ -363,10 +446,10 @@ __global__ void __launch_bounds__(64) ttt_finalize(const float* chunks, float* g
     if (k < K) gdst[(size_t)k * hd] = acc[k] / (float)((k + 1) * (k + 1));
 }
 
-template <bool DYN, typename XT, typename OT, int KP>
+template <class G, bool DYN, bool SOFT, typename XT, typename OT, int KP>
 hipError_t launch_all(const FwdParams& p, float* grad, hipStream_t stream) {
   const unsigned grid = (unsigned)p.n_lb_pad * (unsigned)p.n_tiles;
-  hipLaunchKernelGGL((cheby_ema_ttt_kernel<DYN, XT, OT, KP>), dim3(grid), dim3(G::THREADS), 0, stream, p);
+  hipLaunchKernelGGL((cheby_ema_ttt_kernel<G, DYN, SOFT, XT, OT, KP>), dim3(grid), dim3(G::THREADS), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int n_chunks = (p.n_tiles + kChunk - 1) / kChunk;
@@ -380,20 +463,33 @@ hipError_t launch_all(const FwdParams& p, float* grad, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <bool DYN, typename XT, typename OT>
+template <class G, bool DYN, typename XT, typename OT>
 hipError_t launch_k(const FwdParams& p, float* grad, int kpad, hipStream_t stream) {
-  return kpad == 4 ? launch_all<DYN, XT, OT, 4>(p, grad, stream) : launch_all<DYN, XT, OT, 8>(p, grad, stream);
+  const bool soft = p.ttt_target == 1;
+  if (kpad == 4)
+    return soft ? launch_all<G, DYN, true, XT, OT, 4>(p, grad, stream) : launch_all<G, DYN, false, XT, OT, 4>(p, grad, stream);
+  return soft ? launch_all<G, DYN, true, XT, OT, 8>(p, grad, stream) : launch_all<G, DYN, false, XT, OT, 8>(p, grad, stream);
+}
+
+// Geometry; must agree with ttt_tile_tokens.
+template <bool DYN, typename XT, typename OT>
+hipError_t launch_geo(const FwdParams& p, float* grad, int tile, int kpad, hipStream_t stream) {
+  if (tile != TttTile::TILE) return hipErrorInvalidValue;
+  return launch_k<TttTile, DYN, XT, OT>(p, grad, kpad, stream);
 }
 
 template <bool DYN>
-hipError_t launch_dt(const FwdParams& p, float* grad, int x_dtype, int out_dtype, int kpad, hipStream_t stream) {
-  if (x_dtype == 0 && out_dtype == 0) return launch_k<DYN, float, float>(p, grad, kpad, stream);
-  if (x_dtype == 0 && out_dtype == 1) return launch_k<DYN, float, __bf16>(p, grad, kpad, stream);
-  if (x_dtype == 1 && out_dtype == 0) return launch_k<DYN, __bf16, float>(p, grad, kpad, stream);
-  return launch_k<DYN, __bf16, __bf16>(p, grad, kpad, stream);
+hipError_t launch_dt(const FwdParams& p, float* grad, int x_dtype, int out_dtype, int tile, int kpad,
+                     hipStream_t stream) {
+  if (x_dtype == 0 && out_dtype == 0) return launch_geo<DYN, float, float>(p, grad, tile, kpad, stream);
+  if (x_dtype == 0 && out_dtype == 1) return launch_geo<DYN, float, __bf16>(p, grad, tile, kpad, stream);
+  if (x_dtype == 1 && out_dtype == 0) return launch_geo<DYN, __bf16, float>(p, grad, tile, kpad, stream);
+  return launch_geo<DYN, __bf16, __bf16>(p, grad, tile, kpad, stream);
 }
 
 }  // namespace
+
+int ttt_tile_tokens(bool, int) { return TttTile::TILE; }
 
 size_t ttt_workspace_bytes(int n_lb, int n_tiles, bool dyn, int K) {
   const int kpad = K <= 4 ? 4 : 8;
@@ -403,10 +499,10 @@ size_t ttt_workspace_bytes(int n_lb, int n_tiles, bool dyn, int K) {
   return slots + ((size_t)n_lb * n_tiles + (size_t)n_lb * n_chunks) * F * kLanes * sizeof(float);
 }
 
-hipError_t launch_ttt(const FwdParams& p, float* grad, int x_dtype, int out_dtype, bool dyn, int kpad,
+hipError_t launch_ttt(const FwdParams& p, float* grad, int x_dtype, int out_dtype, bool dyn, int tile, int kpad,
                       hipStream_t stream) {
-  return dyn ? launch_dt<true>(p, grad, x_dtype, out_dtype, kpad, stream)
-             : launch_dt<false>(p, grad, x_dtype, out_dtype, kpad, stream);
+  return dyn ? launch_dt<true>(p, grad, x_dtype, out_dtype, tile, kpad, stream)
+             : launch_dt<false>(p, grad, x_dtype, out_dtype, tile, kpad, stream);
 }
 
 }  // namespace osm
