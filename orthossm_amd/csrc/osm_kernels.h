@@ -42,8 +42,11 @@ constexpr int kMaxFwdTile = FwdTileLarge::TILE;
 // Tokens per forward tile for a launch with n_lb lane-blocks over S tokens.
 int fwd_tile_tokens(bool dyn, int64_t n_lb, int64_t S);
 // TTT: keeps the raw x and r = 1/(1+exp(2 damping p)) of every token of the
-// run in registers, plus 2K gradient accumulators per lane: 8-token runs.
-using TttTile = TileGeo<2, 8, 8>;   // 128 tokens
+// run in registers, plus 2K gradient accumulators per lane: one lane per
+// thread (half the accumulators of two), 16-token runs.  Chosen by
+// measurement on MI355X at BASELINE configs[4] against 2 lanes x 8 or 16
+// tokens and 1 lane x 32 tokens (which spills).
+using TttTile = TileGeo<1, 8, 16>;   // 128 tokens
 int ttt_tile_tokens(bool dyn, int x_dtype);
 
 // Workspace: a kHeaderBytes header (launch epoch, fault word, completion

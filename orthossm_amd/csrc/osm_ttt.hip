@@ -33,31 +33,75 @@ __host__ __device__ constexpr int n_fields() {
   return 2 * KP + 2;  // P_0..P_{KP-1}, Q_0..Q_{KP-1}, Ar (beta), Br (alpha)
 }
 
-// One row of a thread's LPT = 2 lanes of x, kept raw between the passes
-// (bf16: both lanes in one register).  opaque() hides the value from the
-// compiler so that pass 2 re-derives u from it instead of keeping pass 1's
-// unpacked x and u alive across the look-back (twice the registers).
-template <typename XT>
-struct XRow;
+// Raw x of a thread's run (R tokens x LPT lanes), kept between the passes.
+// Pass 1 reads row r with first(r, i), then calls seal(r): from then on the
+// row is read with get(r, i).  seal() hides the value from the compiler, so
+// pass 2 re-derives u from it instead of keeping pass 1's unpacked x and u
+// alive across the look-back (twice the registers); for bf16 with one lane
+// per thread it also packs two tokens per register.
+template <typename XT, int R, int LPT>
+struct XRun;
 
-template <>
-struct XRow<float> {
-  float v[2];
-  __device__ __forceinline__ void zero() { v[0] = v[1] = 0.0f; }
-  __device__ __forceinline__ void load(Rsrc r, uint32_t vo, uint32_t so) { BufVec<float, 2>::load(r, vo, so, v); }
-  __device__ __forceinline__ float get(int i) const { return v[i]; }
-  __device__ __forceinline__ void opaque() { asm volatile("" : "+v"(v[0]), "+v"(v[1])); }
+template <int R, int LPT>
+struct XRun<float, R, LPT> {
+  float v[R][LPT];
+  __device__ __forceinline__ void load_all(const TileAddr& a) {
+    uint32_t so = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      BufVec<float, LPT>::load(a.x, a.vx, so, v[r]);
+      so = next_off(so, a.sx);
+    }
+  }
+  __device__ __forceinline__ float first(int r, int i) const { return v[r][i]; }
+  __device__ __forceinline__ void seal(int r) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) asm volatile("" : "+v"(v[r][i]));
+  }
+  __device__ __forceinline__ float get(int r, int i) const { return v[r][i]; }
 };
 
-template <>
-struct XRow<__bf16> {
-  unsigned v;
-  __device__ __forceinline__ void zero() { v = 0u; }
-  __device__ __forceinline__ void load(Rsrc r, uint32_t vo, uint32_t so) {
-    v = __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, kNT);
+template <int R>
+struct XRun<__bf16, R, 2> {
+  unsigned v[R];   // both lanes of a row
+  __device__ __forceinline__ void load_all(const TileAddr& a) {
+    uint32_t so = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      v[r] = __builtin_amdgcn_raw_buffer_load_b32(a.x, a.vx, so, kNT);
+      so = next_off(so, a.sx);
+    }
   }
-  __device__ __forceinline__ float get(int i) const { return __uint_as_float(i == 0 ? v << 16 : v & 0xffff0000u); }
-  __device__ __forceinline__ void opaque() { asm volatile("" : "+v"(v)); }
+  __device__ __forceinline__ float get(int r, int i) const {
+    return __uint_as_float(i == 0 ? v[r] << 16 : v[r] & 0xffff0000u);
+  }
+  __device__ __forceinline__ float first(int r, int i) const { return get(r, i); }
+  __device__ __forceinline__ void seal(int r) { asm volatile("" : "+v"(v[r])); }
+};
+
+template <int R>
+struct XRun<__bf16, R, 1> {
+  static_assert(R % 2 == 0, "token pairs");
+  unsigned raw[R];     // as loaded (low 16 bits)
+  unsigned v[R / 2];   // rows 2m, 2m+1 packed, once sealed
+  __device__ __forceinline__ void load_all(const TileAddr& a) {
+    uint32_t so = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      raw[r] = __builtin_amdgcn_raw_buffer_load_b16(a.x, a.vx, so, kNT);
+      so = next_off(so, a.sx);
+    }
+  }
+  __device__ __forceinline__ float first(int r, int) const { return __uint_as_float(raw[r] << 16); }
+  __device__ __forceinline__ void seal(int r) {
+    if (r & 1) {
+      v[r / 2] = raw[r - 1] | (raw[r] << 16);
+      asm volatile("" : "+v"(v[r / 2]));
+    }
+  }
+  __device__ __forceinline__ float get(int r, int) const {
+    return __uint_as_float((r & 1) ? v[r / 2] & 0xffff0000u : v[r / 2] << 16);
+  }
 };
 
 // Target y of one x value.
@@ -82,7 +126,7 @@ struct RunGrad {
 // (e = 0 where |s| > 1), the sequence end (e = 0 for t >= S-1) and the
 // ema_final capture; the fast variant assumes none of them occurs in the run.
 template <class G, bool DYN, bool SOFT, bool SLOW, typename XT, typename OT, int KP>
-__device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G::LPT], const XRow<XT> (&xr)[G::R],
+__device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G::LPT], const XRun<XT, G::R, G::LPT>& xr,
                                           const float (&rr)[G::R][G::LPT], const float (&lamv)[G::R],
                                           const float (&y_after)[G::LPT], const TileAddr& a, float lo, float hi,
                                           int t_first, int S, bool clamp, float* fin) {
@@ -96,7 +140,7 @@ __device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G:
   rg.Lp = 1.0f;
   float u[LPT];
 #pragma unroll
-  for (int i = 0; i < LPT; ++i) u[i] = softsign_fast(xr[0].get(i));
+  for (int i = 0; i < LPT; ++i) u[i] = softsign_fast(xr.get(0, i));
   uint32_t so = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -108,7 +152,7 @@ __device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G:
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       if (r + 1 < R) {
-        const float xn = xr[r + 1].get(i);
+        const float xn = xr.get(r + 1, i);
         un[i] = softsign_fast(xn);
         yn[i] = SOFT ? ((xn == xn) ? un[i] : xn) : xn;
       } else {
@@ -130,7 +174,7 @@ __device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G:
         const int t = t_first + r;
         const bool pass = !clamp || __builtin_fabsf(s[i]) <= 1.0f;
         e = (t < S - 1 && pass) ? e : 0.0f;
-        const bool ok = xr[r].get(i) == xr[r].get(i);
+        const bool ok = xr.get(r, i) == xr.get(r, i);
         D = ok ? D : 0.0f;
         uu = ok ? uu : 0.0f;
         if (fin && t == S - 1) fin[i] = s[i];
@@ -177,7 +221,6 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   constexpr int NTG = G::NTG;
   constexpr int WORDS = DYN ? 2 : 1;
   constexpr int F = n_fields<KP>();
-  static_assert(LPT == 2, "XRow holds two lanes");
   static_assert(KP <= G::WAVES, "one wave per monomial coefficient");
   __shared__ ChainLds<G> L;
   __shared__ float mono[KP][kLanes];
@@ -199,15 +242,8 @@ cheby_ema_ttt_kernel(const FwdParams p) {
 
   // x rows of the run (raw), g (dynamic lambda), and for the tile's last run
   // the row after the tile (its target y and lambda).
-  XRow<XT> xr[R];
-  {
-    uint32_t so = 0;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      xr[r].load(a.x, a.vx, so);
-      so = next_off(so, a.sx);
-    }
-  }
+  XRun<XT, R, LPT> xr;
+  xr.load_all(a);
   const float lam_h = p.lam[a.h];
   float lamv[R];
   if constexpr (DYN) {
@@ -221,11 +257,12 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     }
   }
   const bool last_run = q.tg == NTG - 1;
-  XRow<XT> x_after;
-  x_after.zero();
+  float x_after[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) x_after[i] = 0.0f;
   float g_after = 0.0f;
   if (last_run) {
-    x_after.load(a.x, a.vx, (uint32_t)R * a.sx);
+    BufVec<XT, LPT>::load(a.x, a.vx, (uint32_t)R * a.sx, x_after);
     if constexpr (DYN) {
       float gv[1];
       BufVec<float, 1>::load(a.g, a.vg, (uint32_t)R * a.sg, gv);
@@ -253,10 +290,11 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     const float n2 = -2.0f * one_m;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      rr[r][i] = tanh_r(horner<KP>(softsign_fast(xr[r].get(i)), c[i]));
+      rr[r][i] = tanh_r(horner<KP>(softsign_fast(xr.first(r, i)), c[i]));
       Bv[i] = __builtin_fmaf(lam, Bv[i], __builtin_fmaf(n2, rr[r][i], one_m));
     }
     A *= lam;
+    xr.seal(r);
   }
   bool bad = false;
 #pragma unroll
@@ -270,7 +308,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
       const float one_m = 1.0f - lamv[r];
 #pragma unroll
       for (int i = 0; i < LPT; ++i) {
-        const float x = xr[r].get(i);
+        const float x = xr.get(r, i);
         if (x != x) rr[r][i] = 0.5f;
         Bv[i] = __builtin_fmaf(lamv[r], Bv[i], __builtin_fmaf(-2.0f * one_m, rr[r][i], one_m));
       }
@@ -279,7 +317,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
 
   // Target and lambda at each run's first token, for the preceding run.
 #pragma unroll
-  for (int i = 0; i < LPT; ++i) sh_y0[q.tg][q.lt * LPT + i] = target_of<SOFT>(xr[0].get(i));
+  for (int i = 0; i < LPT; ++i) sh_y0[q.tg][q.lt * LPT + i] = target_of<SOFT>(xr.get(0, i));
   sh_lam0[q.tg][q.lt] = lamv[0];
 
   unsigned long long* lane_slots = p.slots + ((size_t)ti.lb * p.n_tiles * kLanes + q.wl) * WORDS;
@@ -305,7 +343,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     lam_after = sh_lam0[q.tg + 1][q.lt];
   } else {
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) y_after[i] = target_of<SOFT>(x_after.get(i));
+    for (int i = 0; i < LPT; ++i) y_after[i] = target_of<SOFT>(x_after[i]);
     lam_after = DYN ? __builtin_amdgcn_fmed3f(__builtin_fmaf(p.lam_shift, g_after, lam_h), p.lam_min, p.lam_max)
                     : lam_h;
   }
@@ -329,8 +367,6 @@ cheby_ema_ttt_kernel(const FwdParams p) {
                    ? p.ema_final + (int64_t)ti.b * p.D + ti.lbd * kLanes + q.lt * LPT
                    : nullptr;
   RunGrad<KP, LPT> rg;
-#pragma unroll
-  for (int r = 0; r < R; ++r) xr[r].opaque();
   if (bad || (clamp && big) || ti.is_last)
     ttt_pass2<G, DYN, SOFT, true, XT, OT, KP>(rg, s, xr, rr, lamv, y_after, a, lo, hi, t_first, p.S, clamp, fin);
   else
