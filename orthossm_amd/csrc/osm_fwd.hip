@@ -97,9 +97,8 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   const TileAddr a = tile_addr<G, DYN, XT, OT>(p, q, ti);
 
   // Monomial coefficients (loads first, converted after the x loads).
-  static_assert(KP <= G::WAVES, "one wave per monomial coefficient");
   __shared__ float mono[KP][kLanes];
-  const MonoLoad ml = mono_issue<KP>(p, q, ti, a);
+  const auto ml = mono_issue<KP, G::WAVES>(p, q, ti, a);
 
   // x rows of this thread's run, g (dynamic lambda).
   float w[R][LPT];
@@ -124,7 +123,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     }
   }
 
-  mono_store<KP>(ml, q, mono);
+  mono_store<KP, G::WAVES>(ml, q, mono);
   __syncthreads();
   float c[LPT][KP];
   mono_read<G, KP>(mono, q, c);

@@ -56,51 +56,58 @@ __device__ __forceinline__ uint32_t next_off(uint32_t off, uint32_t step) {
 }
 
 // Monomial coefficients of the series for the tile's 64 lanes, scaled by
-// 2*log2(e)*damping (the tanh argument in exp2 units).  Wave j < KP forms
-// coefficient j of every lane from <= 4 Chebyshev coefficients (kChebMono)
-// in float64 and shares it through LDS.  Split in three steps so the caller
-// can issue these loads before its bulk loads (the conversion then waits only
-// for them) and convert after issuing those:
-//   MonoLoad m = mono_issue(...);  <bulk loads>;  mono_store(m, ...);
+// 2*log2(e)*damping (the tanh argument in exp2 units).  Wave w forms
+// coefficients j = w, w + WAVES, ... < KP of every lane from <= 4 Chebyshev
+// coefficients each (kChebMono) in float64 and shares them through LDS.
+// Split in three steps so the caller can issue these loads before its bulk
+// loads (the conversion then waits only for them) and convert after issuing
+// those:
+//   auto m = mono_issue(...);  <bulk loads>;  mono_store(m, ...);
 //   __syncthreads();  mono_read(...)
+template <int KP, int WAVES>
 struct MonoLoad {
-  float cm[4];
+  static constexpr int NJ = (KP + WAVES - 1) / WAVES;
+  float cm[NJ][4];
   float kap;
-  int j;   // coefficient of this wave (wave-uniform); >= KP: none
+  int w;   // wave index (wave-uniform)
 };
 
-template <int KP>
-__device__ __forceinline__ MonoLoad mono_issue(const FwdParams& p, const ThreadPos& q, const TileInfo& ti,
-                                               const TileAddr& a) {
-  MonoLoad m;
-  m.j = __builtin_amdgcn_readfirstlane(q.wave);
-  m.kap = 0.0f;
+template <int KP, int WAVES>
+__device__ __forceinline__ MonoLoad<KP, WAVES> mono_issue(const FwdParams& p, const ThreadPos& q,
+                                                          const TileInfo& ti, const TileAddr& a) {
+  MonoLoad<KP, WAVES> m;
+  m.w = __builtin_amdgcn_readfirstlane(q.wave);
+  const int d = ti.lbd * kLanes + q.wl;
+  const bool ok = d < p.D;
+  const int h = ok ? d / p.hd : 0;
+  const uint32_t vc = ok ? (uint32_t)(((int64_t)h * p.c_sh + (d - h * p.hd)) * 4) : kOffOOB;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) m.cm[i] = 0.0f;
-  if (m.j < KP) {
-    const int d = ti.lbd * kLanes + q.wl;
-    const bool ok = d < p.D;
-    const int h = ok ? d / p.hd : 0;
-    const uint32_t vc = ok ? (uint32_t)(((int64_t)h * p.c_sh + (d - h * p.hd)) * 4) : kOffOOB;
+  for (int n = 0; n < m.NJ; ++n) {
+    const int j = m.w + n * WAVES;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int k = m.j + 2 * i;
-      float v[1];
-      BufVec<float, 1>::load(a.c, k < p.K ? vc : kOffOOB, (uint32_t)k * a.sc, v);
-      m.cm[i] = v[0];
+      const int k = j + 2 * i;
+      float v[1] = {0.0f};
+      if (j < KP) BufVec<float, 1>::load(a.c, k < p.K ? vc : kOffOOB, (uint32_t)k * a.sc, v);
+      m.cm[n][i] = v[0];
     }
-    m.kap = kTwoLog2e * p.damping[h];
   }
+  m.kap = kTwoLog2e * p.damping[h];
   return m;
 }
 
-template <int KP>
-__device__ __forceinline__ void mono_store(const MonoLoad& m, const ThreadPos& q, float (&mono)[KP][kLanes]) {
-  if (m.j < KP) {
-    double acc = 0.0;
+template <int KP, int WAVES>
+__device__ __forceinline__ void mono_store(const MonoLoad<KP, WAVES>& m, const ThreadPos& q,
+                                           float (&mono)[KP][kLanes]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc = __builtin_fma((double)kChebMono[m.j][i], (double)m.cm[i], acc);
-    mono[m.j][q.wl] = (float)(acc * (double)m.kap);
+  for (int n = 0; n < m.NJ; ++n) {
+    const int j = m.w + n * WAVES;
+    if (j < KP) {
+      double acc = 0.0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc = __builtin_fma((double)kChebMono[j][i], (double)m.cm[n][i], acc);
+      mono[j][q.wl] = (float)(acc * (double)m.kap);
+    }
   }
 }
 

@@ -221,7 +221,6 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   constexpr int NTG = G::NTG;
   constexpr int WORDS = DYN ? 2 : 1;
   constexpr int F = n_fields<KP>();
-  static_assert(KP <= G::WAVES, "one wave per monomial coefficient");
   __shared__ ChainLds<G> L;
   __shared__ float mono[KP][kLanes];
   __shared__ float sh_y0[NTG][kLanes];      // target y at each run's first token
@@ -238,7 +237,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     return;
   }
   const TileAddr a = tile_addr<G, DYN, XT, OT>(p, q, ti);
-  const MonoLoad ml = mono_issue<KP>(p, q, ti, a);
+  const auto ml = mono_issue<KP, G::WAVES>(p, q, ti, a);
 
   // x rows of the run (raw), g (dynamic lambda), and for the tile's last run
   // the row after the tile (its target y and lambda).
@@ -270,7 +269,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     }
   }
 
-  mono_store<KP>(ml, q, mono);
+  mono_store<KP, G::WAVES>(ml, q, mono);
   __syncthreads();
   float c[LPT][KP];
   mono_read<G, KP>(mono, q, c);
