@@ -5,7 +5,8 @@
  *
  *   u = x / (1 + |x|)                               softsign
  *   p = sum_{k<K} c[b,h,k,j] T_k(u)                 Clenshaw, K <= 8
- *   z = tanh(damping[h] * p)                        (z = 0 where x is NaN)
+ *   z = tanh(damping[h] * p)                        (z = 0 where x is NaN, or u = 0
+ *                                                    with OSM_FLAG_NAN_ZERO_U)
  *   s[t] = lam[b,t,h] s[t-1] + (1 - lam[b,t,h]) z   s[-1] = ema_init (0 if NULL)
  *   out  = clamp(s, -1, 1)                          (OSM_FLAG_NO_CLAMP disables)
  *   lam[b,t,h] = lam_h, or clamp(lam_h + lam_shift * g[b,t,h], lam_min, lam_max)
@@ -70,7 +71,10 @@ typedef enum osm_status {
 } osm_status;
 
 /* flags */
-#define OSM_FLAG_NO_CLAMP 0x1 /* out = s instead of clamp(s, -1, 1) */
+#define OSM_FLAG_NO_CLAMP 0x1   /* out = s instead of clamp(s, -1, 1) */
+#define OSM_FLAG_NAN_ZERO_U 0x2 /* a NaN x counts as u = 0 (the reference's PyTorch
+                                   fast path, sdpc_kernel.py:1725) instead of
+                                   giving z = 0 (its Triton kernels, 2086) */
 
 /* TTT target y */
 typedef enum osm_ttt_target { OSM_TARGET_X = 0, OSM_TARGET_SOFTSIGN = 1 } osm_ttt_target;

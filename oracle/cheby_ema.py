@@ -16,7 +16,9 @@ Reference lines each piece restates (paths relative to the reference root):
 * softsign            sdpc_kernel.py:1722-1725 (PyTorch path) and
                       sdpc_kernel.py:2020-2027 (Triton path).  The spec form
                       x/(1+|x|) is used; +-Inf maps to +-1.
-* NaN policy          sdpc_kernel.py:2086: a NaN input gives z = 0.
+* NaN policy          sdpc_kernel.py:2086: a NaN input gives z = 0
+                      (nan_policy "zero_z"); or, as the PyTorch fast path
+                      sdpc_kernel.py:1725, u = 0 (nan_policy "zero_u").
 * Clenshaw            sdpc_kernel.py:1139-1156 (b_k = c_k + 2u b_{k+1} - b_{k+2},
                       p = c_0 + u b_1 - b_2), equal to the basis+einsum form of
                       sdpc_kernel.py:1728-1731, 1751-1776.
@@ -121,7 +123,7 @@ def lambda_field(lam, B, S, H, g=None, lam_shift=0.004, lam_min=0.9, lam_max=0.9
 
 
 def forward(x, coeffs, damping, lam, *, g=None, lam_shift=0.004, lam_min=0.9,
-            lam_max=0.9999, ema_init=None, clamp_out=True, return_parts=False):
+            lam_max=0.9999, ema_init=None, clamp_out=True, return_parts=False, nan_policy="zero_z"):
     """Cheby-RKV forward in float64.
 
     x [B,S,D]; coeffs [B,H,K,hd]; damping [H]; lam [H]; g optional [S,H] or
@@ -140,7 +142,10 @@ def forward(x, coeffs, damping, lam, *, g=None, lam_shift=0.004, lam_min=0.9,
     p = clenshaw(cl[:, None, :, :], uc)                        # [B,S,D]
     delta = np.repeat(np.asarray(damping, dtype=np.float64), hd)  # [D]
     z = np.tanh(delta * p)
-    z = np.where(nan, 0.0, z)                                  # sdpc_kernel.py:2086
+    if nan_policy == "zero_z":
+        z = np.where(nan, 0.0, z)                              # sdpc_kernel.py:2086
+    else:
+        assert nan_policy == "zero_u"                          # sdpc_kernel.py:1725
     lam_t = lambda_field(lam, B, S, H, g, lam_shift, lam_min, lam_max)
     lam_d = np.repeat(lam_t, hd, axis=2)                       # [B,S,D]
     s = np.empty_like(z)
@@ -173,7 +178,7 @@ def forward_chunked(x, coeffs, damping, lam, chunk, **kw):
 
 
 def ttt_grad(x, coeffs, damping, lam, *, g=None, lam_shift=0.004, lam_min=0.9,
-             lam_max=0.9999, ema_init=None, target="x"):
+             lam_max=0.9999, ema_init=None, target="x", nan_policy="zero_z"):
     """TTT coefficient gradient by the closed-form adjoint, float64.
 
     loss = mean over (b, t<S-1, d) of (clamp(s[b,t,d]) - y[b,t+1,d])^2 with
@@ -184,14 +189,15 @@ def ttt_grad(x, coeffs, damping, lam, *, g=None, lam_shift=0.004, lam_min=0.9,
         gL[t]  = 2/N (out[t] - y[t+1]) * [|s[t]| <= 1]   (t < S-1), 0 at S-1
         a[t]   = gL[t] + lam[t+1] a[t+1]
         dp[t]  = (1 - lam[t]) a[t] (1 - z[t]^2) delta_h
-        dc_k   = sum_t dp[t] T_k(u[t])      (u = 0 where x is NaN, dp = 0 there)
+        dc_k   = sum_t dp[t] T_k(u[t])      (u = 0 where x is NaN; dp = 0 there
+                                              under nan_policy "zero_z")
     """
     x = np.asarray(x, dtype=np.float64)
     B, S, D = x.shape
     _, H, K, hd = np.shape(coeffs)
     out, ema_final, parts = forward(x, coeffs, damping, lam, g=g, lam_shift=lam_shift,
                                     lam_min=lam_min, lam_max=lam_max, ema_init=ema_init,
-                                    return_parts=True)
+                                    return_parts=True, nan_policy=nan_policy)
     s, z, lam_t = parts["s"], parts["z"], parts["lam_t"]
     nan = np.isnan(x)
     u = np.where(nan, 0.0, parts["u"])
@@ -210,7 +216,8 @@ def ttt_grad(x, coeffs, damping, lam, *, g=None, lam_shift=0.004, lam_min=0.9,
         a[:, t, :] = acc
     delta = np.repeat(np.asarray(damping, dtype=np.float64), hd)
     dp = (1.0 - lam_d) * a * (1.0 - z * z) * delta
-    dp = np.where(nan, 0.0, dp)
+    if nan_policy == "zero_z":
+        dp = np.where(nan, 0.0, dp)
     Tk = chebyshev_basis(u, K)                                 # [B,S,D,K]
     dc = np.einsum("bsd,bsdk->bdk", dp, Tk)                    # [B,D,K]
     G = dc.reshape(B, H, hd, K).transpose(0, 1, 3, 2)

@@ -17,6 +17,7 @@ MAX_K = 8
 F32 = 0
 BF16 = 1
 FLAG_NO_CLAMP = 0x1
+FLAG_NAN_ZERO_U = 0x2
 TARGET_X = 0
 TARGET_SOFTSIGN = 1
 

@@ -46,7 +46,8 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
   if (!a) return fail(OSM_E_ARG, "args is NULL");
   if (a->abi_version != OSM_ABI_VERSION)
     return fail(OSM_E_ARG, "abi_version %d does not match library ABI %d", a->abi_version, OSM_ABI_VERSION);
-  if (a->flags & ~OSM_FLAG_NO_CLAMP) return fail(OSM_E_ARG, "unknown flag bits 0x%x", a->flags);
+  if (a->flags & ~(OSM_FLAG_NO_CLAMP | OSM_FLAG_NAN_ZERO_U))
+    return fail(OSM_E_ARG, "unknown flag bits 0x%x", a->flags);
   if (a->B < 0 || a->S < 0) return fail(OSM_E_SHAPE, "B=%lld and S=%lld must be >= 0", (long long)a->B, (long long)a->S);
   if (a->H < 1 || a->hd < 4 || a->hd % 4 != 0)
     return fail(OSM_E_SHAPE, "need H >= 1 and hd a positive multiple of 4 (H=%lld hd=%lld)", (long long)a->H,
@@ -145,6 +146,7 @@ osm::FwdParams make_params(const osm_cheby_args* a, const Geometry& geo, void* w
   p.lam_min = a->lam_min;
   p.lam_max = a->lam_max;
   p.clamp_out = (a->flags & OSM_FLAG_NO_CLAMP) ? 0 : 1;
+  p.nan_zero_u = (a->flags & OSM_FLAG_NAN_ZERO_U) ? 1 : 0;
   return p;
 }
 

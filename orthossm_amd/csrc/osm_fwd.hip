@@ -21,13 +21,16 @@
 namespace osm {
 namespace {
 
-// Exact input for the rare path (see pass1_exact): NaN x -> w = 0 as
-// sdpc_kernel.py:2086, +-Inf -> u = +-1.
+// Exact input for the rare path (see pass1_exact): +-Inf -> u = +-1; NaN x
+// -> w = 0 as sdpc_kernel.py:2086, or (nan_zero_u) u = 0 as
+// sdpc_kernel.py:1725.
 template <int KP>
-__device__ __forceinline__ float ema_input_exact(float x, const float (&a)[KP], float one_m, float neg2_one_m) {
-  const float r = tanh_r(horner<KP>(softsign(x), a));
+__device__ __forceinline__ float ema_input_exact(float x, const float (&a)[KP], float one_m, float neg2_one_m,
+                                                 bool nan_zero_u) {
+  const bool ok = x == x;
+  const float r = tanh_r(horner<KP>(ok ? softsign(x) : 0.0f, a));
   const float w = __builtin_fmaf(neg2_one_m, r, one_m);
-  return (x == x) ? w : 0.0f;
+  return (ok || nan_zero_u) ? w : 0.0f;
 }
 
 // Rare path: a run whose aggregate is NaN saw a NaN or infinite input (or
@@ -35,7 +38,7 @@ __device__ __forceinline__ float ema_input_exact(float x, const float (&a)[KP], 
 // special-value handling.
 template <class G, bool DYN, typename XT, int KP>
 __device__ __forceinline__ void pass1_exact(float (&w)[G::R][G::LPT], const TileAddr& a, const float (&c)[G::LPT][KP],
-                                            const float (&lamv)[G::R], float (&Bv)[G::LPT]) {
+                                            const float (&lamv)[G::R], float (&Bv)[G::LPT], bool nan_zero_u) {
 #pragma unroll
   for (int i = 0; i < G::LPT; ++i) Bv[i] = 0.0f;
   for (int r = 0; r < G::R; ++r) {
@@ -46,7 +49,7 @@ __device__ __forceinline__ void pass1_exact(float (&w)[G::R][G::LPT], const Tile
     const float n2 = -2.0f * one_m;
 #pragma unroll
     for (int i = 0; i < G::LPT; ++i) {
-      w[r][i] = ema_input_exact<KP>(xv[i], c[i], one_m, n2);
+      w[r][i] = ema_input_exact<KP>(xv[i], c[i], one_m, n2, nan_zero_u);
       Bv[i] = __builtin_fmaf(lam, Bv[i], w[r][i]);
     }
   }
@@ -182,7 +185,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   bool bad = false;
 #pragma unroll
   for (int i = 0; i < LPT; ++i) bad |= Bv[i] != Bv[i];
-  if (bad) pass1_exact<G, DYN, XT, KP>(w, a, c, lamv, Bv);
+  if (bad) pass1_exact<G, DYN, XT, KP>(w, a, c, lamv, Bv, p.nan_zero_u != 0);
 
   unsigned long long* lane_slots = p.slots + ((size_t)ti.lb * p.n_tiles * kLanes + q.wl) * WORDS;
   const size_t tile_stride = (size_t)kLanes * WORDS;

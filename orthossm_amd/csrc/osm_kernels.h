@@ -75,6 +75,7 @@ struct FwdParams {
   int n_tiles;                 // ceil(S / TILE)
   float lam_shift, lam_min, lam_max;
   int clamp_out;
+  int nan_zero_u;              // NaN x counts as u = 0 (else z = 0)
   float ttt_scale;             // 2 / (B*(S-1)*D)
   int ttt_target;
 };

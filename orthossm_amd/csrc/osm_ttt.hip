@@ -122,14 +122,14 @@ struct RunGrad {
 
 // Pass 2 over a thread's run, in token order: the EMA from the carried state
 // s, out = clamp(s), e[t] = out[t] - y[t+1], and the gradient accumulators.
-// SLOW handles, per element, NaN inputs (D = 0, u = 0), a binding clamp
+// SLOW handles, per element, NaN inputs (u = 0; D = 0 unless nan_zero_u), a binding clamp
 // (e = 0 where |s| > 1), the sequence end (e = 0 for t >= S-1) and the
 // ema_final capture; the fast variant assumes none of them occurs in the run.
 template <class G, bool DYN, bool SOFT, bool SLOW, typename XT, typename OT, int KP>
 __device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G::LPT], const XRun<XT, G::R, G::LPT>& xr,
                                           const float (&rr)[G::R][G::LPT], const float (&lamv)[G::R],
                                           const float (&y_after)[G::LPT], const TileAddr& a, float lo, float hi,
-                                          int t_first, int S, bool clamp, float* fin) {
+                                          int t_first, int S, bool clamp, bool nan_zero_u, float* fin) {
   constexpr int R = G::R, LPT = G::LPT;
 #pragma unroll
   for (int k = 0; k < KP; ++k)
@@ -175,7 +175,7 @@ __device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G:
         const bool pass = !clamp || __builtin_fabsf(s[i]) <= 1.0f;
         e = (t < S - 1 && pass) ? e : 0.0f;
         const bool ok = xr.get(r, i) == xr.get(r, i);
-        D = ok ? D : 0.0f;
+        D = (ok || nan_zero_u) ? D : 0.0f;
         uu = ok ? uu : 0.0f;
         if (fin && t == S - 1) fin[i] = s[i];
       }
@@ -299,7 +299,8 @@ cheby_ema_ttt_kernel(const FwdParams p) {
 #pragma unroll
   for (int i = 0; i < LPT; ++i) bad |= Bv[i] != Bv[i];
   if (bad) {
-    // A NaN input: z = 0 there (r = 1/2 gives w = 0); recompute the aggregate.
+    // A NaN input: z = 0 there (r = 1/2 gives w = 0), or u = 0 with
+    // nan_zero_u; recompute the aggregate.
 #pragma unroll
     for (int i = 0; i < LPT; ++i) Bv[i] = 0.0f;
 #pragma unroll
@@ -308,7 +309,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
 #pragma unroll
       for (int i = 0; i < LPT; ++i) {
         const float x = xr.get(r, i);
-        if (x != x) rr[r][i] = 0.5f;
+        if (x != x) rr[r][i] = p.nan_zero_u ? tanh_r(c[i][0]) : 0.5f;
         Bv[i] = __builtin_fmaf(lamv[r], Bv[i], __builtin_fmaf(-2.0f * one_m, rr[r][i], one_m));
       }
     }
@@ -367,9 +368,11 @@ cheby_ema_ttt_kernel(const FwdParams p) {
                    : nullptr;
   RunGrad<KP, LPT> rg;
   if (bad || (clamp && big) || ti.is_last)
-    ttt_pass2<G, DYN, SOFT, true, XT, OT, KP>(rg, s, xr, rr, lamv, y_after, a, lo, hi, t_first, p.S, clamp, fin);
+    ttt_pass2<G, DYN, SOFT, true, XT, OT, KP>(rg, s, xr, rr, lamv, y_after, a, lo, hi, t_first, p.S, clamp,
+                                               p.nan_zero_u != 0, fin);
   else
-    ttt_pass2<G, DYN, SOFT, false, XT, OT, KP>(rg, s, xr, rr, lamv, y_after, a, lo, hi, t_first, p.S, clamp, fin);
+    ttt_pass2<G, DYN, SOFT, false, XT, OT, KP>(rg, s, xr, rr, lamv, y_after, a, lo, hi, t_first, p.S, clamp,
+                                                false, fin);
 
   // Compose the runs of the tile: rho of run g = Ar_g + Br_g rho_tile.
   const float beta = rg.Lp * lam_after;

@@ -51,7 +51,8 @@ def _dtype_code(dt: torch.dtype) -> int:
     raise TypeError(f"unsupported dtype {dt}; use float32 or bfloat16")
 
 
-def _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, clamp, out_dtype, out):
+def _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, clamp, out_dtype, out,
+             nan_policy="zero_z"):
     if not isinstance(x, torch.Tensor) or x.dim() != 3:
         raise ValueError("x must be a [B,S,D] tensor")
     if x.device.type != "cuda":
@@ -91,7 +92,9 @@ def _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, 
         raise ValueError("out must have a contiguous lane dimension and 4-element aligned rows")
     a = nat.ChebyArgs()
     a.abi_version = nat.ABI_VERSION
-    a.flags = 0 if clamp else nat.FLAG_NO_CLAMP
+    if nan_policy not in ("zero_z", "zero_u"):
+        raise ValueError("nan_policy must be 'zero_z' or 'zero_u'")
+    a.flags = (0 if clamp else nat.FLAG_NO_CLAMP) | (nat.FLAG_NAN_ZERO_U if nan_policy == "zero_u" else 0)
     a.B, a.S, a.H, a.hd, a.K = B, S, H, hd, K
     a.x, a.x_dtype, a.x_stride_b, a.x_stride_s = x.data_ptr(), _dtype_code(x.dtype), x.stride(0), x.stride(1)
     a.out, a.out_dtype = out.data_ptr(), _dtype_code(out.dtype)
@@ -111,18 +114,21 @@ def cheby_ema_forward(x: torch.Tensor, coeffs: torch.Tensor, damping: Sequence[f
                       lam_shift: float = 0.004, lam_min: float = 0.9, lam_max: float = 0.9999,
                       ema_init: torch.Tensor | None = None, clamp: bool = True,
                       out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
-                      return_state: bool = False, state_out: torch.Tensor | None = None):
+                      return_state: bool = False, state_out: torch.Tensor | None = None,
+                      nan_policy: str = "zero_z"):
     """Fused softsign -> Clenshaw -> damping -> tanh -> EMA on the GPU.
 
     x [B,S,D] fp32|bf16, coeffs [B,H,K,hd] fp32, damping/lam [H], g optional
     [S,H] or [B,S,H] (dynamic lambda), ema_init optional [B,D].
     Returns out [B,S,D] (dtype of x unless out_dtype), and ema_final [B,D]
     fp32 when return_state.  ``state_out`` (contiguous [B,D] fp32 on the
-    device) receives ema_final instead of a new tensor.
+    device) receives ema_final instead of a new tensor.  ``nan_policy``: a
+    NaN input gives z = 0 ('zero_z', the reference's Triton kernels) or counts
+    as u = 0 ('zero_u', the reference's PyTorch fast path).
     """
     lib = nat.load()
     a, out, keep = _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, clamp,
-                            out_dtype, out)
+                            out_dtype, out, nan_policy)
     dev = out.device
     ema_final = _state_buffer(a, dev, return_state, state_out)
     stream = torch.cuda.current_stream(dev).cuda_stream
@@ -141,7 +147,7 @@ def cheby_ema_ttt(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, *, g: tor
                   ema_init: torch.Tensor | None = None, target: str = "x", clamp: bool = True,
                   out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None,
                   return_state: bool = False, state_out: torch.Tensor | None = None,
-                  grad_out: torch.Tensor | None = None):
+                  grad_out: torch.Tensor | None = None, nan_policy: str = "zero_z"):
     """Fused forward plus the TTT coefficient gradient
     grad[b,h,k,j] = d/dc MSE(out[:, :-1], y[:, 1:]) / (k+1)^2, y = x ('x') or
     softsign(x) ('softsign').  Returns (out, grad) or (out, grad, ema_final).
@@ -152,7 +158,7 @@ def cheby_ema_ttt(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, *, g: tor
     if tgt is None:
         raise ValueError("target must be 'x' or 'softsign'")
     a, out, keep = _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, clamp,
-                            out_dtype, out)
+                            out_dtype, out, nan_policy)
     dev = out.device
     if grad_out is None:
         grad = torch.empty((a.B, a.H, a.K, a.hd), device=dev, dtype=torch.float32)

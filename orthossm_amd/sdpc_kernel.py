@@ -6,7 +6,8 @@ Reference: sdpc_kernel.py:2522-2606 (public op), alias
 Covered: the fixed-coefficient path the reference takes when
 ``S < seq_threshold`` (``_fast_path_forward``, sdpc_kernel.py:1708-1744):
 stable softsign, Chebyshev evaluation, damping 0.98 - 0.06*h/H, tanh, EMA
-with the scalar momentum ``ema_momentum`` on every head, output clamp; the
+with the scalar momentum ``ema_momentum`` on every head, output clamp, and a
+NaN input counted as u = 0 as that path does (sdpc_kernel.py:1725); the
 coefficients and momentum come back unchanged (cast to fp32, as
 sdpc_kernel.py:2549-2552).  The Chebyshev series is evaluated exactly
 (the reference's fast path also evaluates it exactly, by basis + einsum).
@@ -52,7 +53,7 @@ def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_m
         raise ValueError(f"D={D} is not divisible by n_heads={H}")
     damping = v10_damping(H, x.device)
     lam = torch.full((H,), float(ema_momentum), dtype=torch.float32, device=x.device)
-    out = cheby_ema_forward(x, coeffs, damping, lam, out_dtype=torch.float32)
+    out = cheby_ema_forward(x, coeffs, damping, lam, out_dtype=torch.float32, nan_policy="zero_u")
     return out, coeffs, momentum_buf
 
 

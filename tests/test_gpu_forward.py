@@ -46,15 +46,16 @@ def test_shapes(dev, B, S, H, hd, K):
     assert_close_fp32(fin.cpu(), wfin, what="ema_final")
 
 
-def test_special_values(dev):
+@pytest.mark.parametrize("nan_policy", ["zero_z", "zero_u"])
+def test_special_values(dev, nan_policy):
     inp = inputs(1, 600, 2, 32, 8, seed=3)
     x = inp["x"]
     specials = [0.0, -0.0, float("inf"), float("-inf"), float("nan"), 1e-42, -1e-42, 3e38, -3e38, 1e30, 1e-7]
     for i, v in enumerate(specials):
         x[0, 10 * i + 5, (7 * i) % 64] = v
     x[0, 400:420, :] = float("nan")          # a run of NaN rows
-    out, fin = run(inp, dev, return_state=True)
-    want, wfin = oracle_forward(inp)
+    out, fin = run(inp, dev, return_state=True, nan_policy=nan_policy)
+    want, wfin = oracle_forward(inp, nan_policy=nan_policy)
     assert_close_fp32(out.cpu(), want)
     assert_close_fp32(fin.cpu(), wfin, what="ema_final")
 

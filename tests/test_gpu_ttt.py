@@ -74,6 +74,24 @@ def test_ttt_with_carry_and_bf16(dev):
     assert_grad(grad, G)
 
 
+@pytest.mark.parametrize("nan_policy", ["zero_z", "zero_u"])
+def test_ttt_nan_inputs(dev, nan_policy):
+    """A NaN input: out follows the NaN policy; the gradient of every lane
+    whose targets contain a NaN is NaN, the other lanes match the oracle."""
+    inp = inputs(1, 700, 2, 32, 8, seed=43)
+    inp["x"][0, 100:104, 5] = float("nan")
+    inp["x"][0, 300, :16] = float("nan")
+    out, grad, fin = run(inp, dev, return_state=True, nan_policy=nan_policy)
+    G, want, wfin = oracle_ttt(inp, nan_policy=nan_policy)
+    assert_close_fp32(out.cpu(), want)
+    assert_close_fp32(fin.cpu(), wfin, what="ema_final")
+    g = grad.cpu().numpy()
+    assert np.array_equal(np.isnan(g), np.isnan(G))
+    ok = ~np.isnan(G)
+    assert ok.any()
+    assert O.rel_err(g[ok], G[ok]) <= 1e-3
+
+
 def test_ttt_forward_matches_forward_kernel(dev):
     inp = to_dev(inputs(2, 5000, 8, 64, 8, seed=41, dynamic=True), dev)
     o1 = cheby_ema_forward(inp["x"], inp["coeffs"], inp["damping"], inp["lam"], g=inp["g"])

@@ -244,10 +244,15 @@ def test_reference_form_agrees_with_oracle():
     out_rf, fin_rf = RF.forward(x, c, damp, lam)
     out_o, fin_o = O.forward(x.numpy(), c.numpy(), damp.numpy(), lam.numpy())
     # The reference form maps a NaN input to u = 0 (sdpc_kernel.py:1725), so
-    # z there is tanh(delta*p(0)) instead of 0: compare the other lanes.
+    # z there is tanh(delta*p(0)) instead of 0: compare the other lanes ...
     mask = np.ones(out_o.shape, bool)
     mask[0, 5:, 3] = False
     assert O.rel_err(out_rf.numpy()[mask], out_o[mask]) < 2e-6
+    assert not np.allclose(out_rf.numpy()[0, 5:, 3], out_o[0, 5:, 3])
+    # ... and every lane under the oracle's "zero_u" policy.
+    out_u, fin_u = O.forward(x.numpy(), c.numpy(), damp.numpy(), lam.numpy(), nan_policy="zero_u")
+    assert O.rel_err(out_rf.numpy(), out_u) < 2e-6
+    assert O.rel_err(fin_rf.numpy(), fin_u) < 2e-6
 
 
 # ---------------------------------------------------------------- mutation checks
