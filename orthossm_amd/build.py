@@ -33,14 +33,22 @@ def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def compile_command(out: str) -> list[str]:
+def common_flags() -> list[str]:
     return [
-        hipcc_path(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+        f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
         "-I", INCLUDE, "-I", CSRC,
-        "-o", out, *sources(),
     ]
+
+
+def compile_command(out: str) -> list[str]:
+    return [hipcc_path(), *common_flags(), "-shared", "-o", out, *sources()]
+
+
+def device_asm_command(src: str, out: str) -> list[str]:
+    """gfx950 assembly of one source (device code only), as the library builds it."""
+    return [hipcc_path(), *common_flags(), "--offload-device-only", "-S", "-o", out, src]
 
 
 def build(verbose: bool = False) -> str:

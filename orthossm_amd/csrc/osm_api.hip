@@ -33,6 +33,7 @@ int ok() {
 struct Geometry {
   int n_lbd = 0, n_lb = 0, n_lb_pad = 0, n_tiles = 0;
   int tile = 0;        // tokens per tile
+  int lanes = 64;      // lanes per lane-block
   bool dyn = false;
   int kpad = 8;
   bool empty = false;  // B == 0 or S == 0
@@ -41,7 +42,7 @@ struct Geometry {
 bool aligned4(const void* p, int esize) { return ((uintptr_t)p % (uintptr_t)(4 * esize)) == 0; }
 
 // Validates `a` without touching the GPU and fills `geo` for the forward
-// (ttt = false; tile size from osm::fwd_tile_tokens) or the TTT kernel.
+// (ttt = false; tile shape from osm::fwd_geometry) or the TTT kernel.
 int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_only = false) {
   if (!a) return fail(OSM_E_ARG, "args is NULL");
   if (a->abi_version != OSM_ABI_VERSION)
@@ -81,7 +82,7 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
       return fail(OSM_E_LAYOUT, "out rows/batches overlap (out_stride_s=%lld < D or out_stride_b too small)",
                   (long long)a->out_stride_s);
     // One tile's byte span must fit a buffer descriptor's 31-bit offsets.
-    const int64_t tile_rows = std::max<int64_t>(osm::kMaxFwdTile, osm::TttTile::TILE) + 1;
+    const int64_t tile_rows = osm::kMaxTileRows + 1;
     if ((tile_rows * a->x_stride_s + D) * xs >= (int64_t(1) << 31) ||
         (tile_rows * a->out_stride_s + D) * os >= (int64_t(1) << 31))
       return fail(OSM_E_LAYOUT, "token stride too large for 31-bit tile offsets");
@@ -95,9 +96,11 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
         a->c_stride_k < 0 || a->c_stride_b < 0)
       return fail(OSM_E_LAYOUT, "coeffs strides must be non-negative and fit 31-bit offsets");
   }
-  const int64_t n_lbd = (D + 63) / 64;
+  osm::FwdShape shape{osm::ttt_tile_tokens(geo->dyn, a->x_dtype), osm::TttTile::LANES};
+  if (!ttt) shape = osm::fwd_geometry(geo->dyn, a->B, D, a->S);
+  const int64_t tile = shape.tile;
+  const int64_t n_lbd = (D + shape.lanes - 1) / shape.lanes;
   const int64_t n_lb = a->B * n_lbd;
-  const int64_t tile = ttt ? osm::ttt_tile_tokens(geo->dyn, a->x_dtype) : osm::fwd_tile_tokens(geo->dyn, n_lb, a->S);
   const int64_t n_tiles = (a->S + tile - 1) / tile;
   const int64_t n_lb_pad = (n_lb + 7) / 8 * 8;
   if (n_lb_pad * n_tiles >= (int64_t(1) << 31) || a->S >= (int64_t(1) << 31) - tile)
@@ -107,6 +110,7 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
   geo->n_lb_pad = (int)n_lb_pad;
   geo->n_tiles = (int)n_tiles;
   geo->tile = (int)tile;
+  geo->lanes = shape.lanes;
   return OSM_OK;
 }
 
@@ -153,7 +157,7 @@ osm::FwdParams make_params(const osm_cheby_args* a, const Geometry& geo, void* w
 size_t ws_bytes_for(const Geometry& geo, bool ttt, int K) {
   if (geo.empty) return osm::kHeaderBytes;
   return ttt ? osm::ttt_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn, K)
-             : osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn);
+             : osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.lanes, geo.dyn);
 }
 
 int check_ws(const Geometry& geo, bool ttt, int K, void* ws, size_t ws_bytes) {
@@ -176,18 +180,19 @@ int hip_fail(hipError_t e, const char* what) {
 // workspace is cleared on the stream first.  A workspace seen for the first
 // time is cleared too, unless osm_workspace_init zeroed it.
 struct Layout {
-  int n_lb, n_tiles, tile, kpad;
+  int n_lb, n_tiles, tile, lanes, kpad;
   bool dyn, ttt;
   bool operator==(const Layout& o) const {
-    return n_lb == o.n_lb && n_tiles == o.n_tiles && tile == o.tile && kpad == o.kpad && dyn == o.dyn && ttt == o.ttt;
+    return n_lb == o.n_lb && n_tiles == o.n_tiles && tile == o.tile && lanes == o.lanes && kpad == o.kpad &&
+           dyn == o.dyn && ttt == o.ttt;
   }
 };
-const Layout kZeroed{-1, -1, -1, false, false};
+const Layout kZeroed{-1, -1, -1, -1, false, false};
 std::mutex g_ws_mu;
 std::unordered_map<uintptr_t, Layout> g_ws_layout;
 
 int prepare_workspace(void* ws, size_t need, const Geometry& geo, bool ttt, hipStream_t stream) {
-  const Layout now{geo.n_lb, geo.n_tiles, geo.tile, geo.kpad, geo.dyn, ttt};
+  const Layout now{geo.n_lb, geo.n_tiles, geo.tile, geo.lanes, geo.kpad, geo.dyn, ttt};
   bool clear;
   {
     std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -251,10 +256,11 @@ int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t worksp
   if (geo.empty) return run_empty(args, st);
   rc = check_ws(geo, false, (int)args->K, workspace, workspace_bytes);
   if (rc != OSM_OK) return rc;
-  rc = prepare_workspace(workspace, osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn), geo, false, st);
+  rc = prepare_workspace(workspace, osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.lanes, geo.dyn), geo, false,
+                         st);
   if (rc != OSM_OK) return rc;
   const osm::FwdParams p = make_params(args, geo, workspace);
-  const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, geo.tile, geo.kpad, st);
+  const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, osm::FwdShape{geo.tile, geo.lanes}, geo.kpad, st);
   if (e != hipSuccess) return hip_fail(e, "forward kernel launch");
   return ok();
 }
@@ -280,7 +286,7 @@ int osm_cheby_ema_ttt(const osm_cheby_args* args, float* grad, int target, void*
   if (rc != OSM_OK) return rc;
   // Only the header and look-back words need clearing: the TTT partials are
   // fully written by every launch before they are read.
-  const size_t slot_bytes = osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn);
+  const size_t slot_bytes = osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.lanes, geo.dyn);
   rc = prepare_workspace(workspace, slot_bytes, geo, true, st);
   if (rc != OSM_OK) return rc;
   osm::FwdParams p = make_params(args, geo, workspace);

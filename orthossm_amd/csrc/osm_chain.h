@@ -4,13 +4,18 @@
 //
 // The EMA s[t] = lam[t] s[t-1] + w[t] composes as affine maps f(s) = A s + B.
 // A tile's aggregate is (A, B) = composition over its tokens from a zero
-// state.  Tiles are grouped in runs of kCkpt = 64; the carry into tile t of
+// state.  Tiles are grouped in runs of G::CKPT; the carry into tile t of
 // group m is
-//     carry = f_{t-1}( ... f_{64m}( C_m ) ... )
-// where C_m is the state after tile 64m-1 (the checkpoint, ema_init for m=0).
-// Every tile publishes its aggregate except the last tile of a group, which
-// publishes its inclusive state as the next checkpoint.  The composition
-// order is fixed, so results do not depend on timing.
+//     carry = f_{t-1}( ... f_{CKPT m}( C_m ) ... )
+// where C_m is the state after tile CKPT m - 1 (the checkpoint, ema_init for
+// m = 0).  Every tile publishes its aggregate except the last tile of a
+// group, which publishes its inclusive state as the next checkpoint.  The
+// composition order is fixed, so results do not depend on timing.
+//
+// A lane-block is G::LANES consecutive lanes of one batch row (64 or 128);
+// the look-back works on 64-lane sub-blocks: sub-block sb is served by waves
+// sb*WPS .. sb*WPS+WPS-1, each reading WPT predecessor tiles, so that
+// CKPT = WPS * WPT.  Look-back words are laid out [lane-block][tile][lane].
 //
 // Tile order.  Virtual tile v covers tile v / n_lb_pad of lane-block
 // v % n_lb_pad, with n_lb_pad = n_lb rounded up to a multiple of 8 (virtual
@@ -31,10 +36,10 @@ namespace osm {
 template <class G>
 struct ChainLds {
   float A[G::NTG][G::TPR];      // token-group aggregate A (one per thread)
-  float B[G::NTG][kLanes];      // token-group aggregate B per lane
-  float mA[G::WAVES][kLanes];   // look-back partial maps per wave
+  float B[G::NTG][G::LANES];    // token-group aggregate B per lane
+  float mA[G::WAVES][kLanes];   // look-back partial maps per wave (lane of its sub-block)
   float mB[G::WAVES][kLanes];
-  float carry[kLanes];          // resolved carry-in of the tile
+  float carry[G::LANES];        // resolved carry-in of the tile
 };
 
 struct TileInfo {
@@ -48,7 +53,8 @@ struct Tags {
 };
 
 // Thread coordinates inside the workgroup: wave, lane in wave (wl), thread in
-// its 64-lane row (lt: lanes lt*LPT .. lt*LPT+LPT-1) and token group (tg).
+// its row (lt: lanes lt*LPT .. lt*LPT+LPT-1 of the lane-block) and token
+// group (tg).
 struct ThreadPos {
   int tid, wave, wl, lt, tg;
 };
@@ -64,6 +70,17 @@ __device__ __forceinline__ ThreadPos thread_pos() {
   return q;
 }
 
+// Lane (within the lane-block) whose look-back words this thread reads, and
+// the lane whose carry it resolves (waves < NSUB only).
+template <class G>
+__device__ __forceinline__ int look_lane(const ThreadPos& q) {
+  return (q.wave / G::WPS) * kLanes + q.wl;
+}
+template <class G>
+__device__ __forceinline__ int carry_lane(const ThreadPos& q) {
+  return q.wave * kLanes + q.wl;
+}
+
 // Launch epoch: constant for the whole launch (the last block bumps it only
 // after every block of this launch has read it).
 __device__ __forceinline__ Tags launch_tags(unsigned* hdr_words) {
@@ -74,6 +91,7 @@ __device__ __forceinline__ Tags launch_tags(unsigned* hdr_words) {
   return t;
 }
 
+template <class G>
 __device__ __forceinline__ TileInfo tile_info(int v, int n_lb, int n_lb_pad, int n_lbd, int n_tiles) {
   TileInfo ti;
   ti.v = v;
@@ -83,8 +101,27 @@ __device__ __forceinline__ TileInfo tile_info(int v, int n_lb, int n_lb_pad, int
   ti.b = ti.lb / n_lbd;
   ti.lbd = ti.lb - ti.b * n_lbd;
   ti.is_last = ti.tile == n_tiles - 1;
-  ti.is_ckpt = (ti.tile % kCkpt) == kCkpt - 1;
+  ti.is_ckpt = (ti.tile % G::CKPT) == G::CKPT - 1;
   return ti;
+}
+
+// Look-back words of one lane-block: [tile][LANES][words].
+struct LaneSlots {
+  unsigned long long* base;   // tile 0, lane 0 of the lane-block
+  size_t tile_stride;         // words per tile
+  int words;                  // 1 (B) or 2 (B, A)
+  __device__ __forceinline__ unsigned long long* at(int tile, int lane) const {
+    return base + (size_t)tile * tile_stride + (size_t)lane * words;
+  }
+};
+
+template <class G, bool DYN>
+__device__ __forceinline__ LaneSlots lane_slots(unsigned long long* slots, const TileInfo& ti, int n_tiles) {
+  LaneSlots s;
+  s.words = DYN ? 2 : 1;
+  s.tile_stride = (size_t)G::LANES * s.words;
+  s.base = slots + (size_t)ti.lb * n_tiles * s.tile_stride;
+  return s;
 }
 
 // Aggregate A of a full tile under a static lambda, in the same
@@ -102,13 +139,12 @@ __device__ __forceinline__ float static_tile_A(float lam) {
 
 // Token-group scan.  In: this thread's run aggregate (A, Bv).  Out: (pA, pB)
 // mapping the tile carry to the state before this thread's first token; in
-// wave 0, (aggA, aggB) = the tile aggregate of lane wl, which is published
-// unless the tile is a checkpoint or the last tile.
+// waves < NSUB, (aggA, aggB) = the tile aggregate of carry_lane(q), which is
+// published unless the tile is a checkpoint or the last tile.
 template <class G, bool DYN>
 __device__ __forceinline__ void tile_scan(ChainLds<G>& L, const ThreadPos& q, const TileInfo& ti, const Tags& tg,
                                           float A, const float (&Bv)[G::LPT], float& pA, float (&pB)[G::LPT],
-                                          float& aggA, float& aggB, unsigned long long* lane_slots,
-                                          size_t tile_stride) {
+                                          float& aggA, float& aggB, const LaneSlots& ls) {
   constexpr int LPT = G::LPT;
   L.A[q.tg][q.lt] = A;
 #pragma unroll
@@ -125,14 +161,15 @@ __device__ __forceinline__ void tile_scan(ChainLds<G>& L, const ThreadPos& q, co
   }
   aggA = 1.0f;
   aggB = 0.0f;
-  if (q.wave == 0) {
+  if (q.wave < G::NSUB) {
+    const int cl = carry_lane<G>(q);
     for (int g = 0; g < G::NTG; ++g) {
-      const float a = L.A[g][q.wl / LPT];
-      aggB = __builtin_fmaf(a, aggB, L.B[g][q.wl]);
+      const float a = L.A[g][cl / LPT];
+      aggB = __builtin_fmaf(a, aggB, L.B[g][cl]);
       aggA *= a;
     }
     if (!ti.is_ckpt && !ti.is_last) {
-      unsigned long long* mine = lane_slots + (size_t)ti.tile * tile_stride;
+      unsigned long long* mine = ls.at(ti.tile, cl);
       if (DYN) publish(mine + 1, tg.agg, aggA);
       publish(mine, tg.agg, aggB);
     }
@@ -143,7 +180,8 @@ __device__ __forceinline__ void tile_scan(ChainLds<G>& L, const ThreadPos& q, co
 // look_back_issue reads (without waiting) the words this thread needs;
 // look_back_finish waits for the ones not yet published, combines, and
 // leaves the carry-in of every lane in L.carry.  Thread (wave, wl) reads
-// lane wl of WPT predecessor tiles; wave 0 also reads the checkpoint.
+// lane look_lane of WPT predecessor tiles; waves < NSUB also read the
+// checkpoint of their carry lane.
 template <class G, bool DYN>
 struct LookBack {
   unsigned long long vB[G::WPT];
@@ -154,36 +192,39 @@ struct LookBack {
 
 template <class G, bool DYN>
 __device__ __forceinline__ void look_back_issue(LookBack<G, DYN>& st, const ThreadPos& q, const TileInfo& ti,
-                                                const unsigned long long* lane_slots, size_t tile_stride) {
-  st.g0 = (ti.tile / kCkpt) * kCkpt;
-  st.beg = st.g0 + q.wave * G::WPT;
+                                                const LaneSlots& ls) {
+  const int ll = look_lane<G>(q);
+  st.g0 = (ti.tile / G::CKPT) * G::CKPT;
+  st.beg = st.g0 + (q.wave % G::WPS) * G::WPT;
   st.end = min(st.beg + G::WPT, ti.tile);
 #pragma unroll
   for (int i = 0; i < G::WPT; ++i) {
     if (st.beg + i < st.end) {
-      const unsigned long long* s = lane_slots + (size_t)(st.beg + i) * tile_stride;
+      const unsigned long long* s = ls.at(st.beg + i, ll);
       st.vB[i] = peek(s);
       if constexpr (DYN) st.vA[i] = peek(s + 1);
     }
   }
   st.vck = 0;
-  if (q.wave == 0 && st.g0 > 0) st.vck = peek(lane_slots + (size_t)(st.g0 - 1) * tile_stride);
+  if (q.wave < G::NSUB && st.g0 > 0) st.vck = peek(ls.at(st.g0 - 1, carry_lane<G>(q)));
 }
 
-// `lam_static_wl` is the static lambda of lane wl (unused when DYN).
+// `lam_look` is the static lambda of look_lane (unused when DYN); `init_carry`
+// the initial state of carry_lane (waves < NSUB).
 template <class G, bool DYN>
 __device__ __forceinline__ void look_back_finish(LookBack<G, DYN>& st, ChainLds<G>& L, const ThreadPos& q,
                                                  const TileInfo& ti, const Tags& tg, float aggA, float aggB,
-                                                 const unsigned long long* lane_slots, size_t tile_stride,
-                                                 float init_wl, float lam_static_wl, unsigned* hdr_words) {
+                                                 const LaneSlots& ls, float init_carry, float lam_look,
+                                                 unsigned* hdr_words) {
   if (ti.tile > 0) {
+    const int ll = look_lane<G>(q);
     float mA = 1.0f, mB = 0.0f;
     if (st.beg < st.end) {
-      const float Afull = DYN ? 1.0f : static_tile_A<G>(lam_static_wl);
+      const float Afull = DYN ? 1.0f : static_tile_A<G>(lam_look);
 #pragma unroll
       for (int i = 0; i < G::WPT; ++i) {
         if (st.beg + i < st.end) {
-          const unsigned long long* s = lane_slots + (size_t)(st.beg + i) * tile_stride;
+          const unsigned long long* s = ls.at(st.beg + i, ll);
           const float Bp = await_word(s, st.vB[i], tg.agg, hdr_words);
           float Ap = Afull;
           if constexpr (DYN) Ap = await_word(s + 1, st.vA[i], tg.agg, hdr_words);
@@ -194,21 +235,21 @@ __device__ __forceinline__ void look_back_finish(LookBack<G, DYN>& st, ChainLds<
     }
     L.mA[q.wave][q.wl] = mA;
     L.mB[q.wave][q.wl] = mB;
-    float ck = init_wl;
-    if (q.wave == 0 && st.g0 > 0)
-      ck = await_word(lane_slots + (size_t)(st.g0 - 1) * tile_stride, st.vck, tg.pre, hdr_words);
+    float ck = init_carry;
+    if (q.wave < G::NSUB && st.g0 > 0)
+      ck = await_word(ls.at(st.g0 - 1, carry_lane<G>(q)), st.vck, tg.pre, hdr_words);
     __syncthreads();
-    if (q.wave == 0) {
+    if (q.wave < G::NSUB) {
+      const int w0 = q.wave * G::WPS;   // the waves that read this sub-block
       float carry = ck;
 #pragma unroll
-      for (int w = 0; w < G::WAVES; ++w) carry = __builtin_fmaf(L.mA[w][q.wl], carry, L.mB[w][q.wl]);
-      L.carry[q.wl] = carry;
+      for (int w = 0; w < G::WPS; ++w) carry = __builtin_fmaf(L.mA[w0 + w][q.wl], carry, L.mB[w0 + w][q.wl]);
+      L.carry[carry_lane<G>(q)] = carry;
       if (ti.is_ckpt && !ti.is_last)
-        publish(const_cast<unsigned long long*>(lane_slots) + (size_t)ti.tile * tile_stride, tg.pre,
-                __builtin_fmaf(aggA, carry, aggB));
+        publish(ls.at(ti.tile, carry_lane<G>(q)), tg.pre, __builtin_fmaf(aggA, carry, aggB));
     }
-  } else if (q.wave == 0) {
-    L.carry[q.wl] = init_wl;
+  } else if (q.wave < G::NSUB) {
+    L.carry[carry_lane<G>(q)] = init_carry;
   }
   __syncthreads();
 }

@@ -15,8 +15,7 @@
 
 namespace osm {
 
-constexpr int kLanes = 64;                // lanes per lane-block
-constexpr int kCkpt = 64;                 // checkpoint interval of the look-back, in tiles
+constexpr int kLanes = 64;                // lanes per look-back sub-block (one wave)
 constexpr float kTwoLog2e = 2.8853900817779268f;  // 2*log2(e): tanh via exp2
 
 // Workspace header (first kHeaderBytes of every workspace).
@@ -231,9 +230,17 @@ struct BufVec<float, 4> {
     const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, kNT);
     v[0] = __uint_as_float(q.x); v[1] = __uint_as_float(q.y); v[2] = __uint_as_float(q.z); v[3] = __uint_as_float(q.w);
   }
+  // A VALU instruction that overwrites the data registers of a store wider
+  // than 64 bits right after it was seen on MI355X to corrupt the store's
+  // first dword now and then (the compiler placed no wait state there), so
+  // the store is followed by two wait states that no instruction can be
+  // scheduled into.
   static __device__ __forceinline__ void store(Rsrc r, uint32_t vo, uint32_t so, const float (&v)[4]) {
     const u32x4 q = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
     __builtin_amdgcn_raw_buffer_store_b128(q, r, vo, so, kNT);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 1");
+    __builtin_amdgcn_sched_barrier(0);
   }
 };
 

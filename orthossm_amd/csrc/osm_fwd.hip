@@ -87,12 +87,11 @@ __global__ void __launch_bounds__(G::THREADS) __attribute__((amdgpu_waves_per_eu
 cheby_ema_fwd_kernel(const FwdParams p) {
   constexpr int R = G::R;
   constexpr int LPT = G::LPT;
-  constexpr int WORDS = DYN ? 2 : 1;
   __shared__ ChainLds<G> L;
 
   const ThreadPos q = thread_pos<G>();
   const Tags tags = launch_tags(p.hdr);
-  const TileInfo ti = tile_info(blockIdx.x, p.n_lb, p.n_lb_pad, p.n_lbd, p.n_tiles);
+  const TileInfo ti = tile_info<G>(blockIdx.x, p.n_lb, p.n_lb_pad, p.n_lbd, p.n_tiles);
   if (ti.pad) {
     finish_block(p.hdr, tags.epoch);
     return;
@@ -100,8 +99,8 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   const TileAddr a = tile_addr<G, DYN, XT, OT>(p, q, ti);
 
   // Monomial coefficients (loads first, converted after the x loads).
-  __shared__ float mono[KP][kLanes];
-  const auto ml = mono_issue<KP, G::WAVES>(p, q, ti, a);
+  __shared__ float mono[KP][G::LANES];
+  const auto ml = mono_issue<KP, G>(p, q, ti, a);
 
   // x rows of this thread's run, g (dynamic lambda).
   float w[R][LPT];
@@ -126,7 +125,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     }
   }
 
-  mono_store<KP, G::WAVES>(ml, q, mono);
+  mono_store<KP, G>(ml, q, mono);
   __syncthreads();
   float c[LPT][KP];
   mono_read<G, KP>(mono, q, c);
@@ -187,19 +186,17 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   for (int i = 0; i < LPT; ++i) bad |= Bv[i] != Bv[i];
   if (bad) pass1_exact<G, DYN, XT, KP>(w, a, c, lamv, Bv, p.nan_zero_u != 0);
 
-  unsigned long long* lane_slots = p.slots + ((size_t)ti.lb * p.n_tiles * kLanes + q.wl) * WORDS;
-  const size_t tile_stride = (size_t)kLanes * WORDS;
+  const LaneSlots ls = lane_slots<G, DYN>(p.slots, ti, p.n_tiles);
   float pA, pB[LPT], aggA, aggB;
-  tile_scan<G, DYN>(L, q, ti, tags, A, Bv, pA, pB, aggA, aggB, lane_slots, tile_stride);
-
-  const int dl = ti.lbd * kLanes + q.wl;
-  const bool dl_ok = dl < p.D;
-  const float init_wl = (p.ema_init && dl_ok) ? p.ema_init[(int64_t)ti.b * p.D + dl] : 0.0f;
-  const float lam_wl = DYN ? 0.0f : p.lam[dl_ok ? dl / p.hd : 0];
+  tile_scan<G, DYN>(L, q, ti, tags, A, Bv, pA, pB, aggA, aggB, ls);
   {
+    const int dc = ti.lbd * G::LANES + carry_lane<G>(q);
+    const float init_c = (p.ema_init && q.wave < G::NSUB && dc < p.D) ? p.ema_init[(int64_t)ti.b * p.D + dc] : 0.0f;
+    const int dlk = ti.lbd * G::LANES + look_lane<G>(q);
+    const float lam_look = DYN ? 0.0f : p.lam[dlk < p.D ? dlk / p.hd : 0];
     LookBack<G, DYN> lbk;
-    look_back_issue<G, DYN>(lbk, q, ti, lane_slots, tile_stride);
-    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, lane_slots, tile_stride, init_wl, lam_wl, p.hdr);
+    look_back_issue<G, DYN>(lbk, q, ti, ls);
+    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, lam_look, p.hdr);
   }
 
   // Pass 2: replay the recurrence from the true carry and store out.
@@ -215,7 +212,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     // from the one run that holds it.
     const int r_last = p.S - 1 - (ti.tile * G::TILE + q.tg * R);
     float* fin = (p.ema_final && a.vo != kOffOOB && r_last >= 0 && r_last < R)
-                     ? p.ema_final + (int64_t)ti.b * p.D + ti.lbd * kLanes + q.lt * LPT
+                     ? p.ema_final + (int64_t)ti.b * p.D + ti.lbd * G::LANES + q.lt * LPT
                      : nullptr;
     pass2<G, OT, true>(s, w, lamv, a, lo, hi, r_last, fin);
   }
@@ -232,21 +229,27 @@ hipError_t launch_g(const FwdParams& p, int kpad, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <class G>
+bool is_shape(FwdShape s) {
+  return s.tile == G::TILE && s.lanes == G::LANES;
+}
+
 template <bool DYN, typename XT, typename OT>
-hipError_t launch_k(const FwdParams& p, int tile, int kpad, hipStream_t stream) {
+hipError_t launch_k(const FwdParams& p, FwdShape s, int kpad, hipStream_t stream) {
   if constexpr (!DYN) {
-    if (tile == FwdTileLarge::TILE) return launch_g<FwdTileLarge, DYN, XT, OT>(p, kpad, stream);
+    if (is_shape<FwdTileLarge>(s)) return launch_g<FwdTileLarge, DYN, XT, OT>(p, kpad, stream);
   }
-  if (tile == FwdTileMedium::TILE) return launch_g<FwdTileMedium, DYN, XT, OT>(p, kpad, stream);
-  return launch_g<FwdTileSmall, DYN, XT, OT>(p, kpad, stream);
+  if (is_shape<FwdTileMedium>(s)) return launch_g<FwdTileMedium, DYN, XT, OT>(p, kpad, stream);
+  if (is_shape<FwdTileSmall>(s)) return launch_g<FwdTileSmall, DYN, XT, OT>(p, kpad, stream);
+  return hipErrorInvalidValue;
 }
 
 template <bool DYN>
-hipError_t launch_dt(const FwdParams& p, int x_dtype, int out_dtype, int tile, int kpad, hipStream_t stream) {
-  if (x_dtype == 0 && out_dtype == 0) return launch_k<DYN, float, float>(p, tile, kpad, stream);
-  if (x_dtype == 0 && out_dtype == 1) return launch_k<DYN, float, __bf16>(p, tile, kpad, stream);
-  if (x_dtype == 1 && out_dtype == 0) return launch_k<DYN, __bf16, float>(p, tile, kpad, stream);
-  return launch_k<DYN, __bf16, __bf16>(p, tile, kpad, stream);
+hipError_t launch_dt(const FwdParams& p, int x_dtype, int out_dtype, FwdShape s, int kpad, hipStream_t stream) {
+  if (x_dtype == 0 && out_dtype == 0) return launch_k<DYN, float, float>(p, s, kpad, stream);
+  if (x_dtype == 0 && out_dtype == 1) return launch_k<DYN, float, __bf16>(p, s, kpad, stream);
+  if (x_dtype == 1 && out_dtype == 0) return launch_k<DYN, __bf16, float>(p, s, kpad, stream);
+  return launch_k<DYN, __bf16, __bf16>(p, s, kpad, stream);
 }
 
 // Grid-stride zero fill (graph-capturable, unlike hipMemsetAsync nodes).
@@ -262,27 +265,29 @@ __global__ void copy_state_kernel(const float* src, float* dst, size_t n) {
 
 }  // namespace
 
-int fwd_tile_tokens(bool dyn, int64_t n_lb, int64_t S) {
-  // Largest tile that still leaves >= kMinTiles workgroups (2 per CU on a
-  // 256-CU MI355X, the residency of the large tile); dynamic lambda holds
-  // more per-token state, so at most the medium tile.
+FwdShape fwd_geometry(bool dyn, int64_t B, int64_t D, int64_t S) {
+  // The largest tile that still leaves >= kMinTiles workgroups with work (2
+  // per CU on a 256-CU MI355X, the residency of the large tile); dynamic
+  // lambda holds more per-token state and is limited to the medium tile.
   constexpr int64_t kMinTiles = 512;
-  const int64_t n_pad = (n_lb + 7) / 8 * 8;
-  if (!dyn && n_pad * ((S + FwdTileLarge::TILE - 1) / FwdTileLarge::TILE) >= kMinTiles) return FwdTileLarge::TILE;
-  if (n_pad * ((S + FwdTileMedium::TILE - 1) / FwdTileMedium::TILE) >= kMinTiles) return FwdTileMedium::TILE;
-  return FwdTileSmall::TILE;
+  auto n_work = [&](int tile, int lanes) { return B * ((D + lanes - 1) / lanes) * ((S + tile - 1) / tile); };
+  if (!dyn && n_work(FwdTileLarge::TILE, FwdTileLarge::LANES) >= kMinTiles)
+    return {FwdTileLarge::TILE, FwdTileLarge::LANES};
+  if (n_work(FwdTileMedium::TILE, FwdTileMedium::LANES) >= kMinTiles)
+    return {FwdTileMedium::TILE, FwdTileMedium::LANES};
+  return {FwdTileSmall::TILE, FwdTileSmall::LANES};
 }
 
 size_t slot_words(bool dyn) { return dyn ? 2 : 1; }
 
-size_t fwd_workspace_bytes(int n_lb, int n_tiles, bool dyn) {
-  return kHeaderBytes + (size_t)n_lb * (size_t)n_tiles * kLanes * slot_words(dyn) * 8;
+size_t fwd_workspace_bytes(int n_lb, int n_tiles, int lanes, bool dyn) {
+  return kHeaderBytes + (size_t)n_lb * (size_t)n_tiles * (size_t)lanes * slot_words(dyn) * 8;
 }
 
-hipError_t launch_fwd(const FwdParams& p, int x_dtype, int out_dtype, bool dyn, int tile, int kpad,
+hipError_t launch_fwd(const FwdParams& p, int x_dtype, int out_dtype, bool dyn, FwdShape shape, int kpad,
                       hipStream_t stream) {
-  return dyn ? launch_dt<true>(p, x_dtype, out_dtype, tile, kpad, stream)
-             : launch_dt<false>(p, x_dtype, out_dtype, tile, kpad, stream);
+  return dyn ? launch_dt<true>(p, x_dtype, out_dtype, shape, kpad, stream)
+             : launch_dt<false>(p, x_dtype, out_dtype, shape, kpad, stream);
 }
 
 hipError_t launch_fill_zero(void* ptr, size_t bytes, hipStream_t stream) {

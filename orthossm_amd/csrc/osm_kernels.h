@@ -10,37 +10,52 @@
 
 namespace osm {
 
-// Tile geometry.  A lane-block is 64 consecutive lanes of one batch row; a
-// tile is TILE consecutive tokens of a lane-block and is one workgroup.  A
-// thread owns LPT adjacent lanes and a run of R consecutive tokens; TPR
-// threads cover the 64 lanes of a row, so one wave instruction reads or
-// writes TGW rows x 256 contiguous bytes (fp32).  Token groups (runs) are
-// ordered wave-major: tg = wave * TGW + lane_in_wave / TPR.
-template <int LPT_, int WAVES_, int R_>
+// Tile geometry.  A lane-block is LANES (64 or 128) consecutive lanes of one
+// batch row; a tile is TILE consecutive tokens of a lane-block and is one
+// workgroup.  A thread owns LPT adjacent lanes and a run of R consecutive
+// tokens; TPR threads cover the LANES lanes of a row, so one wave instruction
+// reads or writes TGW rows x LANES*4 contiguous bytes (fp32).  Token groups
+// (runs) are ordered wave-major: tg = wave * TGW + lane_in_wave / TPR.  The
+// look-back serves each 64-lane sub-block with WPS waves of WPT words per
+// thread, so tiles are grouped in checkpoint runs of CKPT = WPS * WPT.
+template <int LPT_, int WAVES_, int R_, int LANES_ = 64>
 struct TileGeo {
   static constexpr int LPT = LPT_;            // lanes per thread
   static constexpr int WAVES = WAVES_;        // waves per workgroup
   static constexpr int R = R_;                // tokens per thread run
+  static constexpr int LANES = LANES_;        // lanes per lane-block
   static constexpr int THREADS = WAVES * 64;
-  static constexpr int TPR = 64 / LPT;        // threads per 64-lane row
+  static constexpr int NSUB = LANES / 64;     // 64-lane look-back sub-blocks
+  static constexpr int TPR = LANES / LPT;     // threads per row
   static constexpr int TGW = 64 / TPR;        // token groups per wave
   static constexpr int NTG = WAVES * TGW;     // token groups per tile
   static constexpr int TILE = NTG * R;        // tokens per tile
-  static constexpr int WPT = 64 / WAVES;      // look-back words per thread (64-tile groups)
-  static_assert(64 % LPT == 0 && 64 % WAVES == 0, "geometry");
+  static constexpr int WPS = WAVES / NSUB;    // look-back waves per sub-block
+  static constexpr int WPT = 8;               // look-back words per thread
+  static constexpr int CKPT = WPS * WPT;      // checkpoint interval, tiles
+  static_assert(LANES % 64 == 0 && LANES % LPT == 0 && TPR <= 64 && 64 % TPR == 0, "geometry");
+  static_assert(WAVES % NSUB == 0, "look-back waves");
 };
 
-// Forward: 2 lanes per thread, 8 waves; the run length sets the tile.
-// Longer runs amortise the per-tile scan and look-back over more tokens but
-// give fewer workgroups, so the host takes the largest tile that still fills
-// the chip (fwd_tile_tokens).  Dynamic lambda keeps a per-token lambda in
-// registers and is limited to the medium tile.
-using FwdTileLarge = TileGeo<2, 8, 32>;    // 512 tokens
-using FwdTileMedium = TileGeo<2, 8, 16>;   // 256 tokens
-using FwdTileSmall = TileGeo<2, 8, 8>;     // 128 tokens
-constexpr int kMaxFwdTile = FwdTileLarge::TILE;
-// Tokens per forward tile for a launch with n_lb lane-blocks over S tokens.
-int fwd_tile_tokens(bool dyn, int64_t n_lb, int64_t S);
+// Forward: the run length sets the tile.  Longer runs amortise the per-tile
+// scan and look-back over more tokens but give fewer workgroups, so the host
+// takes the largest tile that still fills the chip (fwd_geometry).  Dynamic
+// lambda keeps a per-token lambda in registers and is limited to the medium
+// tile.  Measured on MI355X at BASELINE configs[1] against 128-lane tiles
+// with 2 or 4 lanes per thread (256 and 128 tokens) and 64-lane tiles with 4
+// lanes per thread: the 64-lane, 2-lane, 512-token tile is fastest.
+using FwdTileLarge = TileGeo<2, 8, 32>;    // 512 tokens x 64 lanes
+using FwdTileMedium = TileGeo<2, 8, 16>;   // 256 tokens x 64 lanes
+using FwdTileSmall = TileGeo<2, 8, 8>;     // 128 tokens x 64 lanes
+constexpr int kMaxTileRows = 512;              // bound on TILE (+1 row read past a tile)
+
+// Geometry of a forward launch.
+struct FwdShape {
+  int tile;    // tokens per tile
+  int lanes;   // lanes per lane-block
+};
+FwdShape fwd_geometry(bool dyn, int64_t B, int64_t D, int64_t S);
+
 // TTT: keeps the raw x and r = 1/(1+exp(2 damping p)) of every token of the
 // run in registers, plus 2K gradient accumulators per lane: one lane per
 // thread (half the accumulators of two), 16-token runs.  Chosen by
@@ -62,14 +77,14 @@ struct FwdParams {
   const float* g;
   const float* ema_init;
   float* ema_final;
-  unsigned long long* slots;   // look-back words [n_lb][n_tiles][64][words]
+  unsigned long long* slots;   // look-back words [n_lb][n_tiles][LANES][words]
   unsigned* hdr;               // WsHeader
   float* partials;             // TTT per-tile partials (TTT kernels only)
   int64_t x_sb, x_ss, o_sb, o_ss;
   int64_t c_sb, c_sh, c_sk;
   int64_t g_sb, g_ss, g_sh;
   int B, S, H, hd, K, D;
-  int n_lbd;                   // lane-blocks per batch row = ceil(D / 64)
+  int n_lbd;                   // lane-blocks per batch row = ceil(D / LANES)
   int n_lb;                    // B * n_lbd
   int n_lb_pad;                // n_lb rounded up to a multiple of 8; grid = n_lb_pad * n_tiles
   int n_tiles;                 // ceil(S / TILE)
@@ -82,11 +97,11 @@ struct FwdParams {
 
 // Workspace layout helpers (bytes).
 size_t slot_words(bool dyn);
-size_t fwd_workspace_bytes(int n_lb, int n_tiles, bool dyn);
+size_t fwd_workspace_bytes(int n_lb, int n_tiles, int lanes, bool dyn);
 size_t ttt_workspace_bytes(int n_lb, int n_tiles, bool dyn, int K);
 
 // Launchers: return hipSuccess or the launch error.
-hipError_t launch_fwd(const FwdParams& p, int x_dtype, int out_dtype, bool dyn, int tile, int kpad,
+hipError_t launch_fwd(const FwdParams& p, int x_dtype, int out_dtype, bool dyn, FwdShape shape, int kpad,
                       hipStream_t stream);
 hipError_t launch_ttt(const FwdParams& p, float* grad, int x_dtype, int out_dtype, bool dyn, int tile,
                       int kpad, hipStream_t stream);

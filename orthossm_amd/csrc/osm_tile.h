@@ -22,7 +22,7 @@ template <class G, bool DYN, typename XT, typename OT>
 __device__ __forceinline__ TileAddr tile_addr(const FwdParams& p, const ThreadPos& q, const TileInfo& ti) {
   TileAddr a;
   const int t_tile = ti.tile * G::TILE;
-  const int d0 = ti.lbd * kLanes + q.lt * G::LPT;
+  const int d0 = ti.lbd * G::LANES + q.lt * G::LPT;
   const bool lane_ok = d0 < p.D;
   const uint64_t rows_after = (uint64_t)(p.S - 1 - t_tile);
   a.h = lane_ok ? d0 / p.hd : 0;
@@ -55,64 +55,68 @@ __device__ __forceinline__ uint32_t next_off(uint32_t off, uint32_t step) {
   return off;
 }
 
-// Monomial coefficients of the series for the tile's 64 lanes, scaled by
-// 2*log2(e)*damping (the tanh argument in exp2 units).  Wave w forms
-// coefficients j = w, w + WAVES, ... < KP of every lane from <= 4 Chebyshev
-// coefficients each (kChebMono) in float64 and shares them through LDS.
+// Monomial coefficients of the series for the tile's lanes, scaled by
+// 2*log2(e)*damping (the tanh argument in exp2 units).  The work is split in
+// units (coefficient j, 64-lane sub-block sb); wave w takes units w, w +
+// WAVES, ... and forms coefficient j of its 64 lanes from <= 4 Chebyshev
+// coefficients (kChebMono) in float64; results are shared through LDS.
 // Split in three steps so the caller can issue these loads before its bulk
 // loads (the conversion then waits only for them) and convert after issuing
 // those:
 //   auto m = mono_issue(...);  <bulk loads>;  mono_store(m, ...);
 //   __syncthreads();  mono_read(...)
-template <int KP, int WAVES>
+template <int KP, class G>
 struct MonoLoad {
-  static constexpr int NJ = (KP + WAVES - 1) / WAVES;
+  static constexpr int NU = KP * G::NSUB;                   // units
+  static constexpr int NJ = (NU + G::WAVES - 1) / G::WAVES;  // units per wave
   float cm[NJ][4];
-  float kap;
+  float kap[NJ];
   int w;   // wave index (wave-uniform)
 };
 
-template <int KP, int WAVES>
-__device__ __forceinline__ MonoLoad<KP, WAVES> mono_issue(const FwdParams& p, const ThreadPos& q,
-                                                          const TileInfo& ti, const TileAddr& a) {
-  MonoLoad<KP, WAVES> m;
+template <int KP, class G>
+__device__ __forceinline__ MonoLoad<KP, G> mono_issue(const FwdParams& p, const ThreadPos& q, const TileInfo& ti,
+                                                      const TileAddr& a) {
+  MonoLoad<KP, G> m;
   m.w = __builtin_amdgcn_readfirstlane(q.wave);
-  const int d = ti.lbd * kLanes + q.wl;
-  const bool ok = d < p.D;
-  const int h = ok ? d / p.hd : 0;
-  const uint32_t vc = ok ? (uint32_t)(((int64_t)h * p.c_sh + (d - h * p.hd)) * 4) : kOffOOB;
 #pragma unroll
   for (int n = 0; n < m.NJ; ++n) {
-    const int j = m.w + n * WAVES;
+    const int u = m.w + n * G::WAVES;
+    const int j = u / G::NSUB;
+    const int d = ti.lbd * G::LANES + (u % G::NSUB) * kLanes + q.wl;
+    const bool ok = u < m.NU && d < p.D;
+    const int h = ok ? d / p.hd : 0;
+    const uint32_t vc = ok ? (uint32_t)(((int64_t)h * p.c_sh + (d - h * p.hd)) * 4) : kOffOOB;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int k = j + 2 * i;
       float v[1] = {0.0f};
-      if (j < KP) BufVec<float, 1>::load(a.c, k < p.K ? vc : kOffOOB, (uint32_t)k * a.sc, v);
+      if (u < m.NU) BufVec<float, 1>::load(a.c, k < p.K ? vc : kOffOOB, (uint32_t)k * a.sc, v);
       m.cm[n][i] = v[0];
     }
+    m.kap[n] = kTwoLog2e * p.damping[h];
   }
-  m.kap = kTwoLog2e * p.damping[h];
   return m;
 }
 
-template <int KP, int WAVES>
-__device__ __forceinline__ void mono_store(const MonoLoad<KP, WAVES>& m, const ThreadPos& q,
-                                           float (&mono)[KP][kLanes]) {
+template <int KP, class G>
+__device__ __forceinline__ void mono_store(const MonoLoad<KP, G>& m, const ThreadPos& q,
+                                           float (&mono)[KP][G::LANES]) {
 #pragma unroll
   for (int n = 0; n < m.NJ; ++n) {
-    const int j = m.w + n * WAVES;
-    if (j < KP) {
+    const int u = m.w + n * G::WAVES;
+    if (u < m.NU) {
+      const int j = u / G::NSUB;
       double acc = 0.0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc = __builtin_fma((double)kChebMono[j][i], (double)m.cm[n][i], acc);
-      mono[j][q.wl] = (float)(acc * (double)m.kap);
+      mono[j][(u % G::NSUB) * kLanes + q.wl] = (float)(acc * (double)m.kap[n]);
     }
   }
 }
 
 template <class G, int KP>
-__device__ __forceinline__ void mono_read(const float (&mono)[KP][kLanes], const ThreadPos& q,
+__device__ __forceinline__ void mono_read(const float (&mono)[KP][G::LANES], const ThreadPos& q,
                                           float (&c)[G::LPT][KP]) {
 #pragma unroll
   for (int j = 0; j < KP; ++j)

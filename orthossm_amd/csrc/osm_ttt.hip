@@ -219,8 +219,8 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   constexpr int R = G::R;
   constexpr int LPT = G::LPT;
   constexpr int NTG = G::NTG;
-  constexpr int WORDS = DYN ? 2 : 1;
   constexpr int F = n_fields<KP>();
+  static_assert(G::LANES == kLanes, "partials and merges assume 64-lane lane-blocks");
   __shared__ ChainLds<G> L;
   __shared__ float mono[KP][kLanes];
   __shared__ float sh_y0[NTG][kLanes];      // target y at each run's first token
@@ -231,13 +231,13 @@ cheby_ema_ttt_kernel(const FwdParams p) {
 
   const ThreadPos q = thread_pos<G>();
   const Tags tags = launch_tags(p.hdr);
-  const TileInfo ti = tile_info(blockIdx.x, p.n_lb, p.n_lb_pad, p.n_lbd, p.n_tiles);
+  const TileInfo ti = tile_info<G>(blockIdx.x, p.n_lb, p.n_lb_pad, p.n_lbd, p.n_tiles);
   if (ti.pad) {
     finish_block(p.hdr, tags.epoch);
     return;
   }
   const TileAddr a = tile_addr<G, DYN, XT, OT>(p, q, ti);
-  const auto ml = mono_issue<KP, G::WAVES>(p, q, ti, a);
+  const auto ml = mono_issue<KP, G>(p, q, ti, a);
 
   // x rows of the run (raw), g (dynamic lambda), and for the tile's last run
   // the row after the tile (its target y and lambda).
@@ -269,7 +269,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     }
   }
 
-  mono_store<KP, G::WAVES>(ml, q, mono);
+  mono_store<KP, G>(ml, q, mono);
   __syncthreads();
   float c[LPT][KP];
   mono_read<G, KP>(mono, q, c);
@@ -320,19 +320,17 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   for (int i = 0; i < LPT; ++i) sh_y0[q.tg][q.lt * LPT + i] = target_of<SOFT>(xr.get(0, i));
   sh_lam0[q.tg][q.lt] = lamv[0];
 
-  unsigned long long* lane_slots = p.slots + ((size_t)ti.lb * p.n_tiles * kLanes + q.wl) * WORDS;
-  const size_t tile_stride = (size_t)kLanes * WORDS;
+  const LaneSlots ls = lane_slots<G, DYN>(p.slots, ti, p.n_tiles);
   float pA, pB[LPT], aggA, aggB;
-  tile_scan<G, DYN>(L, q, ti, tags, A, Bv, pA, pB, aggA, aggB, lane_slots, tile_stride);  // syncs sh_y0 too
-
-  const int dl = ti.lbd * kLanes + q.wl;
-  const bool dl_ok = dl < p.D;
-  const float init_wl = (p.ema_init && dl_ok) ? p.ema_init[(int64_t)ti.b * p.D + dl] : 0.0f;
-  const float lam_wl = DYN ? 0.0f : p.lam[dl_ok ? dl / p.hd : 0];
+  tile_scan<G, DYN>(L, q, ti, tags, A, Bv, pA, pB, aggA, aggB, ls);  // syncs sh_y0 too
   {
+    const int dc = ti.lbd * G::LANES + carry_lane<G>(q);
+    const float init_c = (p.ema_init && q.wave < G::NSUB && dc < p.D) ? p.ema_init[(int64_t)ti.b * p.D + dc] : 0.0f;
+    const int dlk = ti.lbd * G::LANES + look_lane<G>(q);
+    const float lam_look = DYN ? 0.0f : p.lam[dlk < p.D ? dlk / p.hd : 0];
     LookBack<G, DYN> lbk;
-    look_back_issue<G, DYN>(lbk, q, ti, lane_slots, tile_stride);
-    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, lane_slots, tile_stride, init_wl, lam_wl, p.hdr);
+    look_back_issue<G, DYN>(lbk, q, ti, ls);
+    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, lam_look, p.hdr);
   }
 
   float y_after[LPT];
@@ -533,7 +531,7 @@ size_t ttt_workspace_bytes(int n_lb, int n_tiles, bool dyn, int K) {
   const int kpad = K <= 4 ? 4 : 8;
   const size_t F = 2 * kpad + 2;
   const size_t n_chunks = (n_tiles + kChunk - 1) / kChunk;
-  const size_t slots = (fwd_workspace_bytes(n_lb, n_tiles, dyn) + 255) / 256 * 256;
+  const size_t slots = (fwd_workspace_bytes(n_lb, n_tiles, TttTile::LANES, dyn) + 255) / 256 * 256;
   return slots + ((size_t)n_lb * n_tiles + (size_t)n_lb * n_chunks) * F * kLanes * sizeof(float);
 }
 

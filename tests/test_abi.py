@@ -68,7 +68,8 @@ def test_workspace_bytes_formula():
     lib = nat.load()
     a = _args()
     # 2048-byte header + one 8-byte word per (lane-block, tile, lane): static
-    # lambda uses 512-token tiles (32 per lane-block at S=16384)
+    # lambda uses 512-token tiles of 64-lane lane-blocks (4 x 8 lane-blocks,
+    # 32 tiles each at S=16384)
     assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 32 * 64 * 8
     # dynamic lambda: 256-token tiles, two words (A and B) per lane
     a.g = 0x10000

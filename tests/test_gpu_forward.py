@@ -37,6 +37,8 @@ def test_config0_cpu_reference_shape(dev):
     (1, 4096, 8, 64, 4),
     (1, 64 * 256 + 77, 2, 32, 8),   # > 64 tiles: crosses a look-back checkpoint
     (2, 3 * 64 * 256 + 5, 1, 64, 8),  # several checkpoints
+    (2, 70001, 4, 64, 8),    # 512-token tiles, three checkpoint groups
+    (3, 20000, 6, 64, 8),    # lane-block count not a multiple of 8
 ])
 def test_shapes(dev, B, S, H, hd, K):
     inp = inputs(B, S, H, hd, K, seed=B * 1000 + S)
