@@ -35,13 +35,17 @@ Reference lines each piece restates (paths relative to the reference root):
                       (README.md:96-97).  Adjoint chain as in
                       sdpc_kernel.py:681-777 (reverse EMA) and 784-915
                       (dL/dy through tanh, Chebyshev basis).
+* backward            dL/dx, dL/dc, dL/d ema_init of (out, ema_final): the
+                      fast path's autograd (sdpc_kernel.py:1708-1744) with the
+                      EMA's masked reverse scan (1677-1701, 682-777).
 
 Pinning (tests/test_oracle.py): Clenshaw against numpy.polynomial.chebyshev
 and cos(k*theta); softsign/tanh special values; the EMA against
 scipy.signal.lfilter and closed forms; dynamic lambda against a brute-force
-loop; the adjoint gradient against torch autograd and central finite
-differences; the whole forward against the reference-form restatement in
-``oracle/reference_form.py``.
+loop; the TTT adjoint gradient and the backward against torch autograd and
+central finite differences (the backward's clamp mask against autograd of a
+state-clamped forward); the whole forward against the reference-form
+restatement in ``oracle/reference_form.py``.
 """
 from __future__ import annotations
 
@@ -223,6 +227,139 @@ def ttt_grad(x, coeffs, damping, lam, *, g=None, lam_shift=0.004, lam_min=0.9,
     G = dc.reshape(B, H, hd, K).transpose(0, 1, 3, 2)
     G = G / (np.arange(1, K + 1, dtype=np.float64) ** 2).reshape(1, 1, K, 1)
     return G, out, ema_final
+
+
+SOFTSIGN_GRAD_MIN = float(np.float32(1e-7))
+
+
+def backward(x, coeffs, damping, lam, grad_out, *, g=None, lam_shift=0.004, lam_min=0.9,
+             lam_max=0.9999, ema_init=None, grad_state=None, clamp_out=True, nan_policy="zero_z",
+             out_saved=None):
+    """Gradients of (out, ema_final) w.r.t. x, coeffs and ema_init, float64,
+    given dL/dout = grad_out [B,S,D] and optionally dL/d ema_final =
+    grad_state [B,D]; lambda (static or dynamic) and damping are constants.
+    Returns (grad_x [B,S,D], grad_coeffs [B,H,K,hd], grad_init [B,D]).
+
+    Restates the reference's gradient of the fast path (sdpc_kernel.py:
+    1708-1744 differentiated by autograd, with the EMA's own backward
+    _EMAFastPathFn.backward 1677-1701 and its reverse scan 682-777)::
+
+        a[t]  = m[t] (dL/dout[t] + lam[t+1] a[t+1]),   a[S] = dL/d ema_final, lam[S] = 1
+        m[t]  = [|out[t]| < 1 - 1e-6]   (out = the saved forward output; m = 1 without the clamp)
+        dp[t] = (1 - lam[t]) a[t] delta (1 - z[t]^2)
+        dL/dc_k       = sum_t dp[t] T_k(u[t])
+        dL/dx[t]      = dp[t] p'(u[t]) / (1 + |x[t]|)^2,  p'(u) = sum_k k c_k U_{k-1}(u)
+        dL/d ema_init = lam[0] a[0]
+
+    The mask gates the carried adjoint as well as dL/dout[t] (the reference
+    scan's affine step is a = m*mu, b = m*g, sdpc_kernel.py:696-702).
+    dL/dx is 0 where |x| < 1e-7 (fp32) and at NaN: the reference clamps |x|
+    at 1e-7 before the softsign (sdpc_kernel.py:1723) and masks NaN with
+    torch.where (1725), so autograd passes no gradient there.  Under
+    nan_policy 'zero_z' a NaN token's z is the constant 0 and adds nothing to
+    dL/dc; under 'zero_u' it adds dp T_k(0).  The reference's full-path
+    backward runs the same adjoint with the static momentum even when the
+    forward used dynamic lambda (sdpc_kernel.py:2443); here lam[t] is the one
+    the forward used."""
+    x = np.asarray(x, dtype=np.float64)
+    B, S, D = x.shape
+    _, H, K, hd = np.shape(coeffs)
+    out, fin, parts = forward(x, coeffs, damping, lam, g=g, lam_shift=lam_shift, lam_min=lam_min,
+                              lam_max=lam_max, ema_init=ema_init, clamp_out=clamp_out, return_parts=True,
+                              nan_policy=nan_policy)
+    z, lam_t = parts["z"], parts["lam_t"]
+    if out_saved is not None:
+        out = np.asarray(out_saved, dtype=np.float64)
+    nan = np.isnan(x)
+    u = np.where(nan, 0.0, parts["u"])
+    go = np.asarray(grad_out, dtype=np.float64)
+    m = (np.abs(out) < 1.0 - 1e-6) if clamp_out else np.ones(out.shape, bool)
+    lam_d = np.repeat(lam_t, hd, axis=2)
+    a = np.empty_like(z)
+    acc = np.zeros((B, D)) if grad_state is None else np.asarray(grad_state, np.float64).reshape(B, D).copy()
+    for t in range(S - 1, -1, -1):
+        lam_next = lam_d[:, t + 1, :] if t + 1 < S else 1.0
+        acc = np.where(m[:, t, :], go[:, t, :] + lam_next * acc, 0.0)
+        a[:, t, :] = acc
+    delta = np.repeat(np.asarray(damping, dtype=np.float64), hd)
+    dp = (1.0 - lam_d) * a * delta * (1.0 - z * z)
+    if nan_policy == "zero_z":
+        dp = np.where(nan, 0.0, dp)
+    Tk = chebyshev_basis(u, K)                                  # [B,S,D,K]
+    gc = np.einsum("bsd,bsdk->bdk", dp, Tk).reshape(B, H, hd, K).transpose(0, 1, 3, 2)
+    # p'(u) from U_{k-1}: U_0 = 1, U_1 = 2u, U_k = 2u U_{k-1} - U_{k-2}
+    cl = lane_coeffs(coeffs)                                    # [B,D,K]
+    U = [np.ones_like(u), 2.0 * u]
+    for _ in range(2, K):
+        U.append(2.0 * u * U[-1] - U[-2])
+    dpdu = np.zeros_like(u)
+    for k in range(1, K):
+        dpdu += k * cl[:, None, :, k] * U[k - 1]
+    with np.errstate(invalid="ignore"):
+        dudx = 1.0 / (1.0 + np.abs(x)) ** 2
+    live = ~nan & (np.abs(x) >= SOFTSIGN_GRAD_MIN)
+    gx = np.where(live, dp * dpdu * dudx, 0.0)
+    gi = lam_d[:, 0, :] * a[:, 0, :]
+    return gx, gc, gi
+
+
+def _forward_torch(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init,
+                   nan_policy="zero_z", state_clamp=None):
+    """The forward as a float64 torch graph (small shapes: the EMA is a
+    loop).  The softsign is written as the reference writes it
+    (sdpc_kernel.py:1722-1725).  With ``state_clamp`` = c the recurrence's
+    state is clamped to [-c, c] at every step and is the output."""
+    import torch
+
+    B, S, D = x.shape
+    _, H, K, hd = coeffs.shape
+    nan = torch.isnan(x)
+    u = x.sign() * (1.0 - 1.0 / (1.0 + x.abs().clamp(min=1e-7)))
+    u = torch.where(nan, torch.zeros_like(u), u)
+    cl = coeffs.permute(0, 1, 3, 2).reshape(B, 1, D, K)
+    T = [torch.ones_like(u), u]
+    for _ in range(2, K):
+        T.append(2.0 * u * T[-1] - T[-2])
+    basis = torch.stack(T[:K], dim=-1)
+    p = (basis * cl).sum(-1)
+    delta = torch.as_tensor(np.repeat(np.asarray(damping, np.float64), hd))
+    z = torch.tanh(delta * p)
+    if nan_policy == "zero_z":
+        z = torch.where(nan, torch.zeros_like(z), z)
+    lam_t = torch.as_tensor(np.ascontiguousarray(lambda_field(lam, B, S, H, g, lam_shift, lam_min, lam_max)))
+    lam_d = lam_t.repeat_interleave(hd, dim=2)
+    state = torch.zeros(B, D, dtype=torch.float64) if ema_init is None else ema_init
+    outs = []
+    for t in range(S):
+        state = lam_d[:, t] * state + (1.0 - lam_d[:, t]) * z[:, t]
+        if state_clamp is not None:
+            state = torch.clamp(state, -state_clamp, state_clamp)
+        outs.append(state)
+    s = torch.stack(outs, dim=1)
+    out = s if state_clamp is not None else torch.clamp(s, -1.0, 1.0)
+    return out, state, u
+
+
+def backward_autograd(x, coeffs, damping, lam, grad_out, *, g=None, lam_shift=0.004, lam_min=0.9,
+                      lam_max=0.9999, ema_init=None, grad_state=None, nan_policy="zero_z",
+                      state_clamp=None):
+    """Same gradients by torch float64 autograd of ``_forward_torch``
+    (small shapes).  Returns (grad_x, grad_coeffs, grad_init, out)."""
+    import torch
+
+    xt = torch.as_tensor(np.asarray(x, dtype=np.float64)).clone().requires_grad_(True)
+    B, S, D = xt.shape
+    c = torch.as_tensor(np.asarray(coeffs, dtype=np.float64)).clone().requires_grad_(True)
+    init = torch.zeros(B, D, dtype=torch.float64) if ema_init is None else \
+        torch.as_tensor(np.asarray(ema_init, np.float64).reshape(B, D))
+    init = init.clone().requires_grad_(True)
+    out, fin, _ = _forward_torch(xt, c, damping, lam, g, lam_shift, lam_min, lam_max, init,
+                                 nan_policy, state_clamp)
+    loss = (out * torch.as_tensor(np.asarray(grad_out, np.float64))).sum()
+    if grad_state is not None:
+        loss = loss + (fin * torch.as_tensor(np.asarray(grad_state, np.float64).reshape(B, D))).sum()
+    loss.backward()
+    return xt.grad.numpy(), c.grad.numpy(), init.grad.numpy(), out.detach().numpy()
 
 
 def ttt_grad_autograd(x, coeffs, damping, lam, *, g=None, lam_shift=0.004, lam_min=0.9,

@@ -231,6 +231,113 @@ def test_ttt_short_sequence_is_zero():
     assert np.all(G == 0)
 
 
+# ---------------------------------------------------------------- backward
+def _bwd_case(B, S, H, hd, K, dyn, seed):
+    r = np.random.default_rng(seed)
+    x = r.standard_normal((B, S, H * hd))
+    c = r.standard_normal((B, H, K, hd)) / np.arange(1, K + 1).reshape(1, 1, K, 1)
+    g = r.uniform(-1, 1, size=(B, S, H)) if dyn else None
+    init = r.uniform(-0.5, 0.5, size=(B, H * hd))
+    go = r.standard_normal(x.shape)
+    gs = r.standard_normal((B, H * hd))
+    return x, c, g, init, go, gs
+
+
+@pytest.mark.parametrize("dyn", [False, True])
+@pytest.mark.parametrize("nan_policy", ["zero_z", "zero_u"])
+def test_backward_matches_autograd(dyn, nan_policy):
+    x, c, g, init, go, gs = _bwd_case(2, 37, 2, 4, 8, dyn, 11)
+    x[0, 5, 3] = np.nan
+    x[1, 9, 0] = 0.0
+    x[1, 10, 6] = np.inf
+    kw = dict(g=g, lam_shift=0.05, ema_init=init, grad_state=gs, nan_policy=nan_policy)
+    gx, gc, gi = O.backward(x, c, [1.0, 0.8], [0.9, 0.97], go, **kw)
+    ax, ac, ai, _ = O.backward_autograd(x, c, [1.0, 0.8], [0.9, 0.97], go, **kw)
+    np.testing.assert_allclose(gx, ax, rtol=1e-10, atol=1e-14)
+    np.testing.assert_allclose(gc, ac, rtol=1e-10, atol=1e-14)
+    np.testing.assert_allclose(gi, ai, rtol=1e-10, atol=1e-14)
+    assert gx[0, 5, 3] == 0 and gx[1, 9, 0] == 0 and gx[1, 10, 6] == 0
+
+
+def test_backward_matches_central_finite_differences():
+    B, S, H, hd, K = 1, 10, 1, 3, 8
+    x, c, _, init, go, gs = _bwd_case(B, S, H, hd, K, False, 12)
+    gx, gc, gi = O.backward(x, c, [0.9], [0.8], go, ema_init=init, grad_state=gs)
+
+    def loss(xx, cc, ii):
+        out, fin = O.forward(xx, cc, [0.9], [0.8], ema_init=ii)
+        return np.sum(out * go) + np.sum(fin * gs)
+
+    def fd(arr, f):
+        d = np.zeros_like(arr)
+        for idx in np.ndindex(arr.shape):
+            ests = []
+            for eps in (1e-4, 3e-5, 1e-5):
+                ap, am = arr.copy(), arr.copy()
+                ap[idx] += eps
+                am[idx] -= eps
+                ests.append((f(ap) - f(am)) / (2 * eps))
+            d[idx] = np.median(ests)
+        return d
+
+    np.testing.assert_allclose(gx, fd(x, lambda a: loss(a, c, init)), rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(gc, fd(c, lambda a: loss(x, a, init)), rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(gi, fd(init, lambda a: loss(x, c, a)), rtol=1e-6, atol=1e-9)
+
+
+def test_backward_tiny_inputs_pass_no_gradient_to_x():
+    x, c, _, _, go, _ = _bwd_case(1, 8, 1, 4, 8, False, 13)
+    x[0, 2, :] = [3e-8, -5e-8, 2e-7, -1e-6]
+    gx, _, _ = O.backward(x, c, [1.0], [0.9], go)
+    ax, _, _, _ = O.backward_autograd(x, c, [1.0], [0.9], go)
+    assert gx[0, 2, 0] == 0 and gx[0, 2, 1] == 0 and gx[0, 2, 2] != 0
+    np.testing.assert_allclose(gx, ax, rtol=1e-9, atol=1e-14)
+
+
+def test_backward_mask_gates_the_carried_adjoint():
+    # Lane 0 saturates (z = 1 exactly, init = 1): every output sits at the
+    # clamp, so the reference's mask zeroes its adjoint, carry included.
+    # Autograd of a forward whose state is clamped at 1 - 1e-6 has the same
+    # gradient; the plain forward's autograd does not (its grad_init is not 0).
+    r = np.random.default_rng(14)
+    x = np.full((1, 30, 2), 5.0)
+    x[:, 20:] = r.standard_normal((1, 10, 2))
+    c = np.zeros((1, 1, 8, 2))
+    c[0, 0, 0] = [30.0, 0.3]
+    c[0, 0, 1] = 1.0
+    go = r.standard_normal(x.shape)
+    init = np.array([[1.0, 0.1]])
+    ax, ac, ai, out_c = O.backward_autograd(x, c, [1.0], [0.9], go, ema_init=init, state_clamp=1 - 1e-6)
+    gx, gc, gi = O.backward(x, c, [1.0], [0.9], go, ema_init=init, out_saved=out_c)
+    np.testing.assert_allclose(gx, ax, atol=1e-14)
+    np.testing.assert_allclose(gc, ac, atol=1e-13)
+    np.testing.assert_allclose(gi, ai, atol=1e-14)
+    assert gi[0, 0] == 0
+    assert O.backward_autograd(x, c, [1.0], [0.9], go, ema_init=init)[2][0, 0] > 0.05
+
+
+def test_backward_chunked_with_carry_equals_monolithic():
+    x, c, g, init, go, gs = _bwd_case(2, 48, 2, 4, 8, True, 15)
+    kw = dict(lam_shift=0.05)
+    gx, gc, gi = O.backward(x, c, [1.0, 0.8], [0.9, 0.97], go, g=g, ema_init=init, grad_state=gs, **kw)
+    # forward carries, then the backward runs chunk by chunk from the end,
+    # each chunk's grad_init becoming the previous chunk's grad_state.
+    bounds = [(0, 17), (17, 30), (30, 48)]
+    inits = [init]
+    for t0, t1 in bounds[:-1]:
+        inits.append(O.forward(x[:, t0:t1], c, [1.0, 0.8], [0.9, 0.97], g=g[:, t0:t1],
+                               ema_init=inits[-1], **kw)[1])
+    gxs, gcs, carry = [], np.zeros_like(gc), gs
+    for (t0, t1), ini in reversed(list(zip(bounds, inits))):
+        a, b, carry = O.backward(x[:, t0:t1], c, [1.0, 0.8], [0.9, 0.97], go[:, t0:t1], g=g[:, t0:t1],
+                                 ema_init=ini, grad_state=carry, **kw)
+        gxs.insert(0, a)
+        gcs += b
+    np.testing.assert_allclose(np.concatenate(gxs, axis=1), gx, rtol=1e-12, atol=1e-15)
+    np.testing.assert_allclose(gcs, gc, rtol=1e-12, atol=1e-15)
+    np.testing.assert_allclose(carry, gi, rtol=1e-12, atol=1e-15)
+
+
 # ---------------------------------------------------------------- reference form
 def test_reference_form_agrees_with_oracle():
     B, S, H, hd, K = 2, 200, 4, 8, 8
