@@ -33,7 +33,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from orthossm_amd import cheby_ema_forward, cheby_ema_ttt  # noqa: E402
+from orthossm_amd import cheby_ema_backward, cheby_ema_forward, cheby_ema_ttt  # noqa: E402
 from orthossm_amd.synthetic import CONFIGS, make_config_inputs  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
@@ -43,17 +43,19 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 
 def algorithmic_bytes(cfg) -> int:
     """Compulsory bytes of one pass: x read + out written + coeffs, damping,
-    lambda, g (dynamic), EMA state in/out, grad (TTT)."""
+    lambda, g (dynamic), EMA state in/out, grad (TTT).  Backward: x, the
+    saved output and dL/dout read, dL/dx written, coeffs read, dL/dc
+    written, dL/d ema_final read and dL/d ema_init written."""
     esz = 2 if cfg.dtype == torch.bfloat16 else 4
     n = cfg.B * cfg.S * cfg.D
-    total = 2 * n * esz
+    total = (4 if cfg.bwd else 2) * n * esz
     total += cfg.B * cfg.H * cfg.K * cfg.hd * 4          # coeffs
     total += 2 * cfg.H * 4                               # damping, lambda
     if cfg.dynamic:
         total += cfg.B * cfg.S * cfg.H * 4               # g [B,S,H]
     launches = cfg.S // cfg.chunk if cfg.chunk else 1
     total += 2 * cfg.B * cfg.D * 4 * launches            # ema_init in, ema_final out per launch
-    if cfg.ttt:
+    if cfg.ttt or cfg.bwd:
         total += cfg.B * cfg.H * cfg.K * cfg.hd * 4      # grad
     return total
 
@@ -69,11 +71,19 @@ def cpu_baseline(cfg):
     c = inp["coeffs"][0:1]
     S = min(cfg.S, 16384)
     x = x[:, :S].contiguous()
+    if cfg.bwd:
+        out, _ = RF.forward(x, c, inp["damping"], inp["lam"])
+        go = torch.randn(x.shape, generator=torch.Generator().manual_seed(1))
+        run = lambda: RF.backward(x, c, inp["damping"], inp["lam"], out, go)      # noqa: E731
+        what = "masked reverse EMA loop + autograd through basis+einsum+tanh (oracle/reference_form.py)"
+    else:
+        run = lambda: RF.forward(x, c, inp["damping"], inp["lam"])                # noqa: E731
+        what = "basis+einsum+tanh and per-head EMA loop (oracle/reference_form.py)"
     RF.forward(x[:, :256], c, inp["damping"], inp["lam"])        # warm-up
     times = []
     for _ in range(2):
         t0 = time.perf_counter()
-        RF.forward(x, c, inp["damping"], inp["lam"])
+        run()
         times.append(time.perf_counter() - t0)
     t = min(times)
     tokens = S
@@ -82,8 +92,7 @@ def cpu_baseline(cfg):
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"one batch row of the workload: B=1 S={S} D={cfg.D} K={cfg.K} fp32, "
-                  f"basis+einsum+tanh and per-head EMA loop (oracle/reference_form.py), best of 2",
+        "sample": f"one batch row of the workload: B=1 S={S} D={cfg.D} K={cfg.K} fp32, {what}, best of 2",
         "gbs": algorithmic_bytes(cfg) / (cfg.B * cfg.S) * tokens / t / 1e9,
         "cpu": platform.processor() or platform.machine(),
         "os_cpu_count": os.cpu_count(),
@@ -124,7 +133,8 @@ def pmc_summary(fetch_path: str, write_path: str, workload: str) -> dict:
     for key, counter, path in (("read", "FETCH_SIZE", fetch_path), ("write", "WRITE_SIZE", write_path)):
         rows = _counter_rows(path, counter)
         ours = [float(r["Counter_Value"]) * 1024 for r in rows
-                if "cheby_ema_fwd_kernel" in r["Kernel_Name"] or "cheby_ema_ttt_kernel" in r["Kernel_Name"]]
+                if any(k in r["Kernel_Name"] for k in ("cheby_ema_fwd_kernel", "cheby_ema_ttt_kernel",
+                                                       "cheby_ema_bwd_kernel"))]
         copies = [float(r["Counter_Value"]) * 1024 for r in rows if "copyBuffer" in r["Kernel_Name"]][-5:]
         if not ours or len(copies) < 5:
             raise SystemExit(f"pmc_summary: {path} lacks kernel or 5 calibration copies for {counter}")
@@ -192,11 +202,22 @@ def main():
     # ping-pong between two state buffers.
     state0 = torch.zeros(cfg.B, cfg.D, device=dev)
     states = [torch.empty_like(state0), torch.empty_like(state0)]
-    grad = torch.empty(cfg.B, cfg.H, cfg.K, cfg.hd, device=dev) if cfg.ttt else None
+    grad = torch.empty(cfg.B, cfg.H, cfg.K, cfg.hd, device=dev) if (cfg.ttt or cfg.bwd) else None
+    if cfg.bwd:
+        # Saved forward outputs and dL/dout per buffer set; dL/dx goes to gxs.
+        gen = torch.Generator(device=dev).manual_seed(1)
+        for x, out in zip(xs, outs):
+            cheby_ema_forward(x, c, damp, lam, g=g, out=out)
+        gos = [torch.randn(x0.shape, device=dev, generator=gen) for _ in range(args.sets)]
+        gxs = [torch.empty_like(x0) for _ in range(args.sets)]
+        torch.cuda.synchronize()
 
     def step(i):
         x, out = xs[i % args.sets], outs[i % args.sets]
-        if cfg.ttt:
+        if cfg.bwd:
+            cheby_ema_backward(x, c, damp, lam, out, gos[i % args.sets], g=g, grad_state=state0,
+                               grad_x_out=gxs[i % args.sets], grad_coeffs_out=grad, grad_init_out=states[0])
+        elif cfg.ttt:
             cheby_ema_ttt(x, c, damp, lam, g=g, out=out, ema_init=state0, state_out=states[0], grad_out=grad)
         elif cfg.chunk:
             prev = state0
@@ -243,7 +264,8 @@ def main():
     achieved_gbs = algo_launch / (mean_kernel_ms * 1e-3) / 1e9
 
     res = {
-        "metric": METRIC if args.workload == "headline" else f"Clenshaw+EMA tokens/s, workload {cfg.name}",
+        "metric": METRIC if args.workload == "headline" else
+        f"Clenshaw+EMA {'backward ' if cfg.bwd else ''}tokens/s, workload {cfg.name}",
         "value": tokens / (ms_per_step * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -259,6 +281,7 @@ def main():
             "workload": f"BASELINE {cfg.name}: B={cfg.B} S={cfg.S} D={cfg.D} H={cfg.H} hd={cfg.hd} K={cfg.K} "
                         f"{'bf16' if cfg.dtype == torch.bfloat16 else 'fp32'}"
                         f"{' dynamic-lambda' if cfg.dynamic else ''}{' +TTT-grad' if cfg.ttt else ''}"
+                        f"{' backward (dL/dx, dL/dc, dL/d ema_init)' if cfg.bwd else ''}"
                         f"{f' as {cfg.S // cfg.chunk} chunks with carry' if cfg.chunk else ''}",
             "B": cfg.B, "S": cfg.S, "D": cfg.D, "H": cfg.H, "K": cfg.K,
             "parallelism": "single GPU",

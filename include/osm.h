@@ -28,6 +28,12 @@
  *                      _parallel_reverse_ema_kernel (sdpc_kernel.py:2463-2471),
  *                      _parallel_backward_clenshaw_kernel_v10 (2487-2500) and
  *                      grad_c_part.sum (2502), fused with the forward.
+ *   osm_cheby_ema_bwd  the backward of the forward: _EMAFastPathFn.backward
+ *                      (sdpc_kernel.py:1677-1701, its masked reverse scan
+ *                      682-777) and autograd through the fast path's softsign,
+ *                      Chebyshev basis, damping and tanh (1722-1739), giving
+ *                      dL/dx, dL/dc and dL/d ema_init from dL/dout and
+ *                      dL/d ema_final.
  *
  * Conventions
  *   - All device pointers are caller-owned; the library allocates nothing.
@@ -39,7 +45,7 @@
  *     calls: a launch counter and tagged look-back words.  The library clears
  *     it on the stream the first time it sees a workspace pointer (unless
  *     osm_workspace_init zeroed it) and whenever the layout changes (shape,
- *     K class, static/dynamic lambda, forward/TTT).  A workspace freed and a new
+ *     K class, static/dynamic lambda, entry point).  A workspace freed and a new
  *     one allocated at the same address must be passed through
  *     osm_workspace_init.  Two calls that overlap in time must not share one
  *     workspace; if they do, every wave still exits (bounded waits) and the
@@ -112,16 +118,44 @@ typedef struct osm_cheby_args {
   float* ema_final;         /* optional [B, H*hd] fp32 contiguous */
 } osm_cheby_args;
 
+/*
+ * Backward arguments (with the forward's osm_cheby_args, whose `out` is the
+ * saved forward output, read for the clamp mask m = [|out| < 1 - 1e-6]; it
+ * may be NULL with OSM_FLAG_NO_CLAMP).  Given dL/dout and dL/d ema_final:
+ *
+ *   a[t] = m[t] (dL/dout[t] + lam[t+1] a[t+1]),  a past the end = dL/d ema_final
+ *   dL/dx[t]  = (1-lam[t]) a[t] damping (1-z^2) p'(u) / (1+|x|)^2   (0 where
+ *               |x| < 1e-7 or x is NaN)
+ *   dL/dc_k   = sum_t (1-lam[t]) a[t] damping (1-z^2) T_k(u[t])
+ *   dL/d ema_init = lam[0] a[0]
+ *
+ * lambda (static or dynamic) and damping are constants.  grad_out has the
+ * dtype of out and grad_x that of x, with the same layout rules as x/out.
+ */
+typedef struct osm_cheby_bwd_args {
+  const void* grad_out;     /* [B,S,H*hd] dL/dout, out_dtype */
+  int64_t go_stride_b, go_stride_s;
+  const float* grad_state;  /* optional [B, H*hd] fp32 contiguous: dL/d ema_final */
+  void* grad_x;             /* [B,S,H*hd] dL/dx, x_dtype (overwritten) */
+  int64_t gx_stride_b, gx_stride_s;
+  float* grad_coeffs;       /* optional [B,H,K,hd] fp32 contiguous (overwritten) */
+  float* grad_init;         /* optional [B, H*hd] fp32 contiguous: dL/d ema_init */
+} osm_cheby_bwd_args;
+
+/* Which entry point a workspace is sized for. */
+typedef enum osm_op { OSM_OP_FWD = 0, OSM_OP_TTT = 1, OSM_OP_BWD = 2 } osm_op;
+
 /* ABI version the library was built with (OSM_ABI_VERSION). */
 int osm_abi_version(void);
 
 /* Thread-local message of the last failing call on this thread ("" if none). */
 const char* osm_last_error(void);
 
-/* Workspace bytes needed by osm_cheby_ema_fwd (ttt = 0) or
- * osm_cheby_ema_ttt (ttt = 1).  Reads only the shape fields, dtypes, K and
- * whether g is NULL; returns 0 if those are invalid. */
-size_t osm_workspace_bytes(const osm_cheby_args* args, int ttt);
+/* Workspace bytes needed by osm_cheby_ema_fwd (op = OSM_OP_FWD),
+ * osm_cheby_ema_ttt (OSM_OP_TTT) or osm_cheby_ema_bwd (OSM_OP_BWD).  Reads
+ * only the shape fields, dtypes, K and whether g is NULL; returns 0 if those
+ * are invalid. */
+size_t osm_workspace_bytes(const osm_cheby_args* args, int op);
 
 /* Zero-fill `bytes` of workspace on `stream` with a fill kernel. */
 int osm_workspace_init(void* workspace, size_t bytes, void* stream);
@@ -133,6 +167,12 @@ int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t worksp
 /* Fused forward + TTT coefficient gradient.  `grad` is [B,H,K,hd] fp32
  * contiguous and is overwritten.  `target` is an osm_ttt_target. */
 int osm_cheby_ema_ttt(const osm_cheby_args* args, float* grad, int target, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* Backward of osm_cheby_ema_fwd: writes grad_x and, when non-NULL,
+ * grad_coeffs and grad_init.  Replaces the backward listed in the header
+ * comment. */
+int osm_cheby_ema_bwd(const osm_cheby_args* args, const osm_cheby_bwd_args* bwd, void* workspace,
                       size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus

@@ -230,6 +230,9 @@ def ttt_grad(x, coeffs, damping, lam, *, g=None, lam_shift=0.004, lam_min=0.9,
 
 
 SOFTSIGN_GRAD_MIN = float(np.float32(1e-7))
+# The reference compares |out| with 1 - 1e-6 on fp32 tensors, so the bound
+# is that value rounded to fp32.
+MASK_BOUND = float(np.float32(1.0 - 1e-6))
 
 
 def backward(x, coeffs, damping, lam, grad_out, *, g=None, lam_shift=0.004, lam_min=0.9,
@@ -245,7 +248,7 @@ def backward(x, coeffs, damping, lam, grad_out, *, g=None, lam_shift=0.004, lam_
     _EMAFastPathFn.backward 1677-1701 and its reverse scan 682-777)::
 
         a[t]  = m[t] (dL/dout[t] + lam[t+1] a[t+1]),   a[S] = dL/d ema_final, lam[S] = 1
-        m[t]  = [|out[t]| < 1 - 1e-6]   (out = the saved forward output; m = 1 without the clamp)
+        m[t]  = [|out[t]| < 1 - 1e-6 (fp32)]   (out = the saved forward output; m = 1 without the clamp)
         dp[t] = (1 - lam[t]) a[t] delta (1 - z[t]^2)
         dL/dc_k       = sum_t dp[t] T_k(u[t])
         dL/dx[t]      = dp[t] p'(u[t]) / (1 + |x[t]|)^2,  p'(u) = sum_k k c_k U_{k-1}(u)
@@ -273,7 +276,7 @@ def backward(x, coeffs, damping, lam, grad_out, *, g=None, lam_shift=0.004, lam_
     nan = np.isnan(x)
     u = np.where(nan, 0.0, parts["u"])
     go = np.asarray(grad_out, dtype=np.float64)
-    m = (np.abs(out) < 1.0 - 1e-6) if clamp_out else np.ones(out.shape, bool)
+    m = (np.abs(out) < MASK_BOUND) if clamp_out else np.ones(out.shape, bool)
     lam_d = np.repeat(lam_t, hd, axis=2)
     a = np.empty_like(z)
     acc = np.zeros((B, D)) if grad_state is None else np.asarray(grad_state, np.float64).reshape(B, D).copy()

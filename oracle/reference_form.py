@@ -23,10 +23,8 @@ from __future__ import annotations
 import torch
 
 
-def forward(x: torch.Tensor, coeffs: torch.Tensor, damping: torch.Tensor, lam: torch.Tensor,
-            ema_init: torch.Tensor | None = None):
-    """x [B,S,D] float32; coeffs [B,H,K,hd]; damping [H]; lam [H].
-    Returns (out [B,S,D], ema_final [B,D])."""
+def _z(x: torch.Tensor, coeffs: torch.Tensor, damping: torch.Tensor) -> torch.Tensor:
+    """softsign -> Chebyshev basis + einsum -> damping -> tanh, [B,S,D]."""
     B, S, D = x.shape
     _, H, K, hd = coeffs.shape
     ax = x.abs().clamp(min=1e-7)
@@ -39,7 +37,16 @@ def forward(x: torch.Tensor, coeffs: torch.Tensor, damping: torch.Tensor, lam: t
     basis = torch.stack(T[:K], dim=-1)                       # [B,S,H,hd,K]
     y = torch.einsum("bsndk,bndk->bsnd", basis, coeffs.permute(0, 1, 3, 2))
     y = y * damping.view(1, 1, H, 1).to(y.dtype)
-    z = torch.tanh(y).reshape(B, S, D)
+    return torch.tanh(y).reshape(B, S, D)
+
+
+def forward(x: torch.Tensor, coeffs: torch.Tensor, damping: torch.Tensor, lam: torch.Tensor,
+            ema_init: torch.Tensor | None = None):
+    """x [B,S,D] float32; coeffs [B,H,K,hd]; damping [H]; lam [H].
+    Returns (out [B,S,D], ema_final [B,D])."""
+    B, S, D = x.shape
+    hd = coeffs.shape[3]
+    z = _z(x, coeffs, damping)
     lam_d = lam.to(z.dtype).repeat_interleave(hd)            # [D]
     one_m = 1.0 - lam_d
     state = torch.zeros(B, D, dtype=z.dtype) if ema_init is None else ema_init.reshape(B, D).to(z.dtype).clone()
@@ -48,3 +55,28 @@ def forward(x: torch.Tensor, coeffs: torch.Tensor, damping: torch.Tensor, lam: t
         state = lam_d * state + one_m * z[:, t]
         out[:, t] = state
     return out.clamp(-1.0, 1.0), state
+
+
+def backward(x: torch.Tensor, coeffs: torch.Tensor, damping: torch.Tensor, lam: torch.Tensor,
+             out: torch.Tensor, grad_out: torch.Tensor):
+    """The reference's gradient of the fast path: the EMA adjoint as its
+    _EMAFastPathFn.backward computes it (sdpc_kernel.py:1677-1701: mask
+    |out| < 1 - 1e-6, adj[t] = m[t] (g[t] + lam adj[t+1]), dL/dz = (1-lam) adj;
+    here as a sequential loop over t with a per-lane lambda), then torch
+    autograd through softsign, basis, einsum, damping and tanh.
+    Returns (grad_x, grad_coeffs)."""
+    B, S, D = x.shape
+    hd = coeffs.shape[3]
+    lam_d = lam.to(grad_out.dtype).repeat_interleave(hd)
+    m = (out.abs() < 1.0 - 1e-6).to(grad_out.dtype)
+    adj = torch.empty_like(grad_out)
+    a = torch.zeros(B, D, dtype=grad_out.dtype)
+    for t in range(S - 1, -1, -1):
+        a = m[:, t] * (grad_out[:, t] + lam_d * a)
+        adj[:, t] = a
+    xg = x.detach().clone().requires_grad_(True)
+    cg = coeffs.detach().clone().requires_grad_(True)
+    with torch.enable_grad():
+        z = _z(xg, cg, damping)
+        z.backward((1.0 - lam_d) * adj)
+    return xg.grad, cg.grad

@@ -1,11 +1,13 @@
 """MI355X-native (gfx950) Cheby-RKV hot path of OrthoSSM.
 
 Fused softsign -> Clenshaw -> per-head damping -> tanh -> per-head EMA scan,
-with dynamic lambda, EMA carry across chunks, bf16 I/O and the fused TTT
-coefficient gradient, implemented as hand-written HIP kernels behind the C
-ABI of ``include/osm.h`` (library ``orthossm_amd/_lib/libosm.so``).
+with dynamic lambda, EMA carry across chunks, bf16 I/O, the fused TTT
+coefficient gradient and the backward, implemented as hand-written HIP
+kernels behind the C ABI of ``include/osm.h`` (library
+``orthossm_amd/_lib/libosm.so``).
 """
-from .ops import cheby_ema_forward, cheby_ema_ttt
+from .ops import cheby_ema, cheby_ema_backward, cheby_ema_forward, cheby_ema_ttt
 from .sdpc_kernel import apply_cheby_rkv_core, apply_cheby_rkv_v10
 
-__all__ = ["cheby_ema_forward", "cheby_ema_ttt", "apply_cheby_rkv_v10", "apply_cheby_rkv_core"]
+__all__ = ["cheby_ema", "cheby_ema_forward", "cheby_ema_backward", "cheby_ema_ttt", "apply_cheby_rkv_v10",
+           "apply_cheby_rkv_core"]

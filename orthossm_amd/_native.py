@@ -20,6 +20,9 @@ FLAG_NO_CLAMP = 0x1
 FLAG_NAN_ZERO_U = 0x2
 TARGET_X = 0
 TARGET_SOFTSIGN = 1
+OP_FWD = 0
+OP_TTT = 1
+OP_BWD = 2
 
 STATUS = {
     0: "OSM_OK",
@@ -39,6 +42,7 @@ EXPORTS = (
     "osm_workspace_init",
     "osm_cheby_ema_fwd",
     "osm_cheby_ema_ttt",
+    "osm_cheby_ema_bwd",
 )
 
 
@@ -79,6 +83,22 @@ class ChebyArgs(ctypes.Structure):
     ]
 
 
+class BwdArgs(ctypes.Structure):
+    """Mirror of ``osm_cheby_bwd_args``."""
+
+    _fields_ = [
+        ("grad_out", ctypes.c_void_p),
+        ("go_stride_b", ctypes.c_int64),
+        ("go_stride_s", ctypes.c_int64),
+        ("grad_state", ctypes.c_void_p),
+        ("grad_x", ctypes.c_void_p),
+        ("gx_stride_b", ctypes.c_int64),
+        ("gx_stride_s", ctypes.c_int64),
+        ("grad_coeffs", ctypes.c_void_p),
+        ("grad_init", ctypes.c_void_p),
+    ]
+
+
 class OsmError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"{STATUS.get(code, code)}: {msg}")
@@ -116,6 +136,9 @@ def load() -> ctypes.CDLL:
         lib.osm_cheby_ema_ttt.restype = ctypes.c_int
         lib.osm_cheby_ema_ttt.argtypes = [ctypes.POINTER(ChebyArgs), ctypes.c_void_p, ctypes.c_int,
                                           ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.osm_cheby_ema_bwd.restype = ctypes.c_int
+        lib.osm_cheby_ema_bwd.argtypes = [ctypes.POINTER(ChebyArgs), ctypes.POINTER(BwdArgs), ctypes.c_void_p,
+                                          ctypes.c_size_t, ctypes.c_void_p]
         got = lib.osm_abi_version()
         if got != ABI_VERSION:
             raise ImportError(f"orthossm_amd: library ABI {got} != binding ABI {ABI_VERSION}; rebuild")

@@ -41,9 +41,9 @@ struct Geometry {
 
 bool aligned4(const void* p, int esize) { return ((uintptr_t)p % (uintptr_t)(4 * esize)) == 0; }
 
-// Validates `a` without touching the GPU and fills `geo` for the forward
-// (ttt = false; tile shape from osm::fwd_geometry) or the TTT kernel.
-int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_only = false) {
+// Validates `a` without touching the GPU and fills `geo` for the entry point
+// `op` (an osm_op; the forward's tile shape comes from osm::fwd_geometry).
+int check_args(const osm_cheby_args* a, Geometry* geo, int op, bool shapes_only = false) {
   if (!a) return fail(OSM_E_ARG, "args is NULL");
   if (a->abi_version != OSM_ABI_VERSION)
     return fail(OSM_E_ARG, "abi_version %d does not match library ABI %d", a->abi_version, OSM_ABI_VERSION);
@@ -63,22 +63,24 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
   geo->kpad = a->K <= 4 ? 4 : 8;
   geo->empty = a->B == 0 || a->S == 0;
   if (geo->empty) return OSM_OK;
+  // The backward reads out only for the clamp mask.
+  const bool need_out = op != OSM_OP_BWD || !(a->flags & OSM_FLAG_NO_CLAMP);
   if (!shapes_only) {
-    if (!a->x || !a->out || !a->coeffs || !a->damping || !a->lam)
+    if (!a->x || (need_out && !a->out) || !a->coeffs || !a->damping || !a->lam)
       return fail(OSM_E_ARG, "x, out, coeffs, damping and lam must be non-NULL");
     const int xs = a->x_dtype == OSM_F32 ? 4 : 2;
     const int os = a->out_dtype == OSM_F32 ? 4 : 2;
     if (!aligned4(a->x, xs) || a->x_stride_b % 4 || a->x_stride_s % 4 || a->x_stride_b < 0 || a->x_stride_s < 0)
       return fail(OSM_E_LAYOUT, "x must be aligned to 4 elements with non-negative strides that are multiples of 4");
-    if (!aligned4(a->out, os) || a->out_stride_b % 4 || a->out_stride_s % 4 || a->out_stride_b < 0 ||
-        a->out_stride_s < 0)
+    if (a->out && (!aligned4(a->out, os) || a->out_stride_b % 4 || a->out_stride_s % 4 || a->out_stride_b < 0 ||
+                   a->out_stride_s < 0))
       return fail(OSM_E_LAYOUT,
                   "out must be aligned to 4 elements with non-negative strides that are multiples of 4");
     if (geo->dyn && !(a->lam_min <= a->lam_max))
       return fail(OSM_E_ARG, "lam_min %g > lam_max %g", (double)a->lam_min, (double)a->lam_max);
     // Rows of out must not overlap (padding rows of the last tile are masked
     // by extent, which needs out_stride_s >= D and batches after all rows).
-    if (a->out_stride_s < D || a->out_stride_b < a->S * a->out_stride_s)
+    if (a->out && (a->out_stride_s < D || a->out_stride_b < a->S * a->out_stride_s))
       return fail(OSM_E_LAYOUT, "out rows/batches overlap (out_stride_s=%lld < D or out_stride_b too small)",
                   (long long)a->out_stride_s);
     // One tile's byte span must fit a buffer descriptor's 31-bit offsets.
@@ -97,7 +99,8 @@ int check_args(const osm_cheby_args* a, Geometry* geo, bool ttt, bool shapes_onl
       return fail(OSM_E_LAYOUT, "coeffs strides must be non-negative and fit 31-bit offsets");
   }
   osm::FwdShape shape{osm::ttt_tile_tokens(geo->dyn, a->x_dtype), osm::TttTile::LANES};
-  if (!ttt) shape = osm::fwd_geometry(geo->dyn, a->B, D, a->S);
+  if (op == OSM_OP_FWD) shape = osm::fwd_geometry(geo->dyn, a->B, D, a->S);
+  if (op == OSM_OP_BWD) shape = osm::FwdShape{osm::bwd_tile_tokens(geo->dyn), osm::BwdTile::LANES};
   const int64_t tile = shape.tile;
   const int64_t n_lbd = (D + shape.lanes - 1) / shape.lanes;
   const int64_t n_lb = a->B * n_lbd;
@@ -154,16 +157,17 @@ osm::FwdParams make_params(const osm_cheby_args* a, const Geometry& geo, void* w
   return p;
 }
 
-size_t ws_bytes_for(const Geometry& geo, bool ttt, int K) {
+size_t ws_bytes_for(const Geometry& geo, int op, int K) {
   if (geo.empty) return osm::kHeaderBytes;
-  return ttt ? osm::ttt_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn, K)
-             : osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.lanes, geo.dyn);
+  if (op == OSM_OP_TTT) return osm::ttt_workspace_bytes(geo.n_lb, geo.n_tiles, geo.dyn, K);
+  if (op == OSM_OP_BWD) return osm::bwd_workspace_bytes(geo.n_lb, geo.n_tiles, K);
+  return osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.lanes, geo.dyn);
 }
 
-int check_ws(const Geometry& geo, bool ttt, int K, void* ws, size_t ws_bytes) {
+int check_ws(const Geometry& geo, int op, int K, void* ws, size_t ws_bytes) {
   if (!ws) return fail(OSM_E_WORKSPACE, "workspace is NULL");
   if ((uintptr_t)ws % 256) return fail(OSM_E_WORKSPACE, "workspace must be 256-byte aligned");
-  const size_t need = ws_bytes_for(geo, ttt, K);
+  const size_t need = ws_bytes_for(geo, op, K);
   if (ws_bytes < need)
     return fail(OSM_E_WORKSPACE, "workspace has %zu bytes, needs %zu", ws_bytes, need);
   return OSM_OK;
@@ -181,18 +185,19 @@ int hip_fail(hipError_t e, const char* what) {
 // time is cleared too, unless osm_workspace_init zeroed it.
 struct Layout {
   int n_lb, n_tiles, tile, lanes, kpad;
-  bool dyn, ttt;
+  bool dyn;
+  int op;
   bool operator==(const Layout& o) const {
     return n_lb == o.n_lb && n_tiles == o.n_tiles && tile == o.tile && lanes == o.lanes && kpad == o.kpad &&
-           dyn == o.dyn && ttt == o.ttt;
+           dyn == o.dyn && op == o.op;
   }
 };
-const Layout kZeroed{-1, -1, -1, -1, false, false};
+const Layout kZeroed{-1, -1, -1, -1, -1, false, -1};
 std::mutex g_ws_mu;
 std::unordered_map<uintptr_t, Layout> g_ws_layout;
 
-int prepare_workspace(void* ws, size_t need, const Geometry& geo, bool ttt, hipStream_t stream) {
-  const Layout now{geo.n_lb, geo.n_tiles, geo.tile, geo.lanes, geo.kpad, geo.dyn, ttt};
+int prepare_workspace(void* ws, size_t need, const Geometry& geo, int op, hipStream_t stream) {
+  const Layout now{geo.n_lb, geo.n_tiles, geo.tile, geo.lanes, geo.kpad, geo.dyn, op};
   bool clear;
   {
     std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -230,10 +235,14 @@ int osm_abi_version(void) { return OSM_ABI_VERSION; }
 
 const char* osm_last_error(void) { return g_err.c_str(); }
 
-size_t osm_workspace_bytes(const osm_cheby_args* args, int ttt) {
+size_t osm_workspace_bytes(const osm_cheby_args* args, int op) {
+  if (op != OSM_OP_FWD && op != OSM_OP_TTT && op != OSM_OP_BWD) {
+    fail(OSM_E_ARG, "op %d is not an osm_op", op);
+    return 0;
+  }
   Geometry geo;
-  if (check_args(args, &geo, ttt != 0, /*shapes_only=*/true) != OSM_OK) return 0;
-  return ws_bytes_for(geo, ttt != 0, (int)args->K);
+  if (check_args(args, &geo, op, /*shapes_only=*/true) != OSM_OK) return 0;
+  return ws_bytes_for(geo, op, (int)args->K);
 }
 
 int osm_workspace_init(void* workspace, size_t bytes, void* stream) {
@@ -250,14 +259,14 @@ int osm_workspace_init(void* workspace, size_t bytes, void* stream) {
 
 int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t workspace_bytes, void* stream) {
   Geometry geo;
-  int rc = check_args(args, &geo, false);
+  int rc = check_args(args, &geo, OSM_OP_FWD);
   if (rc != OSM_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (geo.empty) return run_empty(args, st);
-  rc = check_ws(geo, false, (int)args->K, workspace, workspace_bytes);
+  rc = check_ws(geo, OSM_OP_FWD, (int)args->K, workspace, workspace_bytes);
   if (rc != OSM_OK) return rc;
-  rc = prepare_workspace(workspace, osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.lanes, geo.dyn), geo, false,
-                         st);
+  rc = prepare_workspace(workspace, osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.lanes, geo.dyn), geo,
+                         OSM_OP_FWD, st);
   if (rc != OSM_OK) return rc;
   const osm::FwdParams p = make_params(args, geo, workspace);
   const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, osm::FwdShape{geo.tile, geo.lanes}, geo.kpad, st);
@@ -268,7 +277,7 @@ int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t worksp
 int osm_cheby_ema_ttt(const osm_cheby_args* args, float* grad, int target, void* workspace,
                       size_t workspace_bytes, void* stream) {
   Geometry geo;
-  int rc = check_args(args, &geo, true);
+  int rc = check_args(args, &geo, OSM_OP_TTT);
   if (rc != OSM_OK) return rc;
   if (!grad && !geo.empty) return fail(OSM_E_ARG, "grad must be non-NULL");
   if (target != OSM_TARGET_X && target != OSM_TARGET_SOFTSIGN)
@@ -282,12 +291,12 @@ int osm_cheby_ema_ttt(const osm_cheby_args* args, float* grad, int target, void*
     }
     return run_empty(args, st);
   }
-  rc = check_ws(geo, true, (int)args->K, workspace, workspace_bytes);
+  rc = check_ws(geo, OSM_OP_TTT, (int)args->K, workspace, workspace_bytes);
   if (rc != OSM_OK) return rc;
   // Only the header and look-back words need clearing: the TTT partials are
   // fully written by every launch before they are read.
   const size_t slot_bytes = osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.lanes, geo.dyn);
-  rc = prepare_workspace(workspace, slot_bytes, geo, true, st);
+  rc = prepare_workspace(workspace, slot_bytes, geo, OSM_OP_TTT, st);
   if (rc != OSM_OK) return rc;
   osm::FwdParams p = make_params(args, geo, workspace);
   p.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((slot_bytes + 255) / 256) * 256);
@@ -295,6 +304,69 @@ int osm_cheby_ema_ttt(const osm_cheby_args* args, float* grad, int target, void*
   p.ttt_target = target;
   const hipError_t e = osm::launch_ttt(p, grad, args->x_dtype, args->out_dtype, geo.dyn, geo.tile, geo.kpad, st);
   if (e != hipSuccess) return hip_fail(e, "TTT kernel launch");
+  return ok();
+}
+
+int osm_cheby_ema_bwd(const osm_cheby_args* args, const osm_cheby_bwd_args* bwd, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  Geometry geo;
+  int rc = check_args(args, &geo, OSM_OP_BWD);
+  if (rc != OSM_OK) return rc;
+  if (!bwd) return fail(OSM_E_ARG, "bwd is NULL");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t D = args->H * args->hd;
+  if (geo.empty) {
+    // No tokens: dL/dc = 0 and ema_final = ema_init, so dL/d ema_init = dL/d ema_final.
+    if (args->B > 0) {
+      hipError_t e = hipSuccess;
+      if (bwd->grad_coeffs)
+        e = osm::launch_fill_zero(bwd->grad_coeffs, (size_t)args->B * args->H * args->K * args->hd * sizeof(float), st);
+      if (e == hipSuccess && bwd->grad_init) {
+        const size_t n = (size_t)args->B * (size_t)D;
+        e = bwd->grad_state ? osm::launch_copy_state(bwd->grad_state, bwd->grad_init, n, st)
+                            : osm::launch_fill_zero(bwd->grad_init, n * sizeof(float), st);
+      }
+      if (e != hipSuccess) return hip_fail(e, "gradient fill launch");
+    }
+    return ok();
+  }
+  if (!bwd->grad_out || !bwd->grad_x) return fail(OSM_E_ARG, "grad_out and grad_x must be non-NULL");
+  const int xs = args->x_dtype == OSM_F32 ? 4 : 2;
+  const int os = args->out_dtype == OSM_F32 ? 4 : 2;
+  if (!aligned4(bwd->grad_out, os) || bwd->go_stride_b % 4 || bwd->go_stride_s % 4 || bwd->go_stride_b < 0 ||
+      bwd->go_stride_s < 0)
+    return fail(OSM_E_LAYOUT,
+                "grad_out must be aligned to 4 elements with non-negative strides that are multiples of 4");
+  if (!aligned4(bwd->grad_x, xs) || bwd->gx_stride_b % 4 || bwd->gx_stride_s % 4)
+    return fail(OSM_E_LAYOUT, "grad_x must be aligned to 4 elements with strides that are multiples of 4");
+  if (bwd->gx_stride_s < D || bwd->gx_stride_b < args->S * bwd->gx_stride_s)
+    return fail(OSM_E_LAYOUT, "grad_x rows/batches overlap (gx_stride_s=%lld < D or gx_stride_b too small)",
+                (long long)bwd->gx_stride_s);
+  const int64_t tile_rows = osm::kMaxTileRows + 1;
+  if ((tile_rows * bwd->go_stride_s + D) * os >= (int64_t(1) << 31) ||
+      (tile_rows * bwd->gx_stride_s + D) * xs >= (int64_t(1) << 31))
+    return fail(OSM_E_LAYOUT, "token stride too large for 31-bit tile offsets");
+  rc = check_ws(geo, OSM_OP_BWD, (int)args->K, workspace, workspace_bytes);
+  if (rc != OSM_OK) return rc;
+  // Only the header and look-back words need clearing: the partials are
+  // fully written by every launch before they are read.
+  const size_t slot_bytes = osm::bwd_slot_bytes(geo.n_lb, geo.n_tiles);
+  rc = prepare_workspace(workspace, slot_bytes, geo, OSM_OP_BWD, st);
+  if (rc != OSM_OK) return rc;
+  osm::BwdParams bp{};
+  bp.f = make_params(args, geo, workspace);
+  bp.f.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((slot_bytes + 255) / 256) * 256);
+  bp.gout = bwd->grad_out;
+  bp.go_sb = bwd->go_stride_b;
+  bp.go_ss = bwd->go_stride_s;
+  bp.gx = bwd->grad_x;
+  bp.gx_sb = bwd->gx_stride_b;
+  bp.gx_ss = bwd->gx_stride_s;
+  bp.grad_state = bwd->grad_state;
+  bp.grad_init = bwd->grad_init;
+  bp.grad_coeffs = bwd->grad_coeffs;
+  const hipError_t e = osm::launch_bwd(bp, args->x_dtype, args->out_dtype, geo.dyn, geo.tile, geo.kpad, st);
+  if (e != hipSuccess) return hip_fail(e, "backward kernel launch");
   return ok();
 }
 

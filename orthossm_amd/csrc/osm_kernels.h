@@ -64,8 +64,16 @@ FwdShape fwd_geometry(bool dyn, int64_t B, int64_t D, int64_t S);
 using TttTile = TileGeo<1, 8, 16>;   // 128 tokens
 int ttt_tile_tokens(bool dyn, int x_dtype);
 
+// Backward: one lane per thread (the clamp mask makes the adjoint map's A
+// differ per lane); x and dL/dout of the run stay in registers between the
+// passes (plus lambda per token with a dynamic lambda).  32-token runs
+// spill at 128 VGPRs; 16-token runs fit in ~100 (static) and ~117 (dynamic).
+using BwdTile = TileGeo<1, 8, 16>;   // 128 tokens
+int bwd_tile_tokens(bool dyn);
+
 // Workspace: a kHeaderBytes header (launch epoch, fault word, completion
-// counters), then the look-back words, then (TTT only) per-tile partials.
+// counters), then the look-back words, then (TTT and backward) per-tile
+// partials.
 constexpr size_t kHeaderBytes = 2048;
 
 struct FwdParams {
@@ -95,16 +103,32 @@ struct FwdParams {
   int ttt_target;
 };
 
+// Backward launch: the forward's parameters (x, out = the saved forward
+// output, coefficients, lambda, shapes, workspace) plus the gradient streams.
+struct BwdParams {
+  FwdParams f;
+  const void* gout;            // dL/dout, dtype of out
+  void* gx;                    // dL/dx, dtype of x
+  int64_t go_sb, go_ss, gx_sb, gx_ss;
+  const float* grad_state;     // dL/d ema_final [B,D] or NULL
+  float* grad_init;            // dL/d ema_init [B,D] or NULL
+  float* grad_coeffs;          // [B,H,K,hd]
+};
+
 // Workspace layout helpers (bytes).
 size_t slot_words(bool dyn);
 size_t fwd_workspace_bytes(int n_lb, int n_tiles, int lanes, bool dyn);
 size_t ttt_workspace_bytes(int n_lb, int n_tiles, bool dyn, int K);
+size_t bwd_workspace_bytes(int n_lb, int n_tiles, int K);
+size_t bwd_slot_bytes(int n_lb, int n_tiles);
 
 // Launchers: return hipSuccess or the launch error.
 hipError_t launch_fwd(const FwdParams& p, int x_dtype, int out_dtype, bool dyn, FwdShape shape, int kpad,
                       hipStream_t stream);
 hipError_t launch_ttt(const FwdParams& p, float* grad, int x_dtype, int out_dtype, bool dyn, int tile,
                       int kpad, hipStream_t stream);
+hipError_t launch_bwd(const BwdParams& p, int x_dtype, int out_dtype, bool dyn, int tile, int kpad,
+                      hipStream_t stream);
 hipError_t launch_fill_zero(void* ptr, size_t bytes, hipStream_t stream);
 hipError_t launch_copy_state(const float* src, float* dst, size_t n, hipStream_t stream);
 

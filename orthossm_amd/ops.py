@@ -1,9 +1,12 @@
 """Torch-facing operators over the C ABI (HIP kernels on gfx950).
 
-``cheby_ema_forward``  fused forward (static or dynamic lambda, EMA carry).
-``cheby_ema_ttt``      fused forward + TTT coefficient gradient.
+``cheby_ema_forward``   fused forward (static or dynamic lambda, EMA carry).
+``cheby_ema_ttt``       fused forward + TTT coefficient gradient.
+``cheby_ema_backward``  dL/dx, dL/dc, dL/d ema_init from dL/dout (+ dL/d ema_final).
+``cheby_ema``           the forward as a differentiable op (autograd.Function
+                        whose backward is ``cheby_ema_backward``).
 
-Both run on the current torch stream of the input's device and never
+All run on the current torch stream of the input's device and never
 synchronise the host.  Inputs are not modified.  There is no CPU path: a
 tensor that is not on a ROCm device raises.
 """
@@ -18,13 +21,15 @@ import torch
 from . import _native as nat
 
 _ws_lock = threading.Lock()
-_ws_cache: dict[tuple[int, int], torch.Tensor] = {}
+_ws_cache: dict[tuple[int, int, int], torch.Tensor] = {}
 
 
-def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    """Zero-initialised workspace reused per (device, stream).  Calls on one
-    stream are ordered, so they never overlap on a workspace."""
-    key = (device.index, stream)
+def _workspace(device: torch.device, stream: int, nbytes: int, op: int) -> torch.Tensor:
+    """Zero-initialised workspace reused per (device, stream, entry point).
+    Calls on one stream are ordered, so they never overlap on a workspace;
+    one workspace per entry point keeps its layout fixed across alternating
+    forward/backward calls (a layout change costs a clear)."""
+    key = (device.index, stream, op)
     with _ws_lock:
         ws = _ws_cache.get(key)
         if ws is None or ws.numel() < nbytes:
@@ -52,7 +57,7 @@ def _dtype_code(dt: torch.dtype) -> int:
 
 
 def _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, clamp, out_dtype, out,
-             nan_policy="zero_z"):
+             nan_policy="zero_z", alloc_out=True):
     if not isinstance(x, torch.Tensor) or x.dim() != 3:
         raise ValueError("x must be a [B,S,D] tensor")
     if x.device.type != "cuda":
@@ -85,10 +90,12 @@ def _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, 
         init = ema_init.to(device=dev, dtype=torch.float32).reshape(B, D).contiguous()
     odt = x.dtype if out_dtype is None else out_dtype
     if out is None:
-        out = torch.empty((B, S, D), device=dev, dtype=odt)
+        if alloc_out:
+            out = torch.empty((B, S, D), device=dev, dtype=odt)
     elif tuple(out.shape) != (B, S, D) or out.dtype != odt or out.device != dev:
         raise ValueError("out has the wrong shape, dtype or device")
-    if out.stride(2) != 1 or out.stride(1) % 4 or out.stride(0) % 4 or out.data_ptr() % (4 * out.element_size()):
+    if out is not None and (out.stride(2) != 1 or out.stride(1) % 4 or out.stride(0) % 4
+                            or out.data_ptr() % (4 * out.element_size())):
         raise ValueError("out must have a contiguous lane dimension and 4-element aligned rows")
     a = nat.ChebyArgs()
     a.abi_version = nat.ABI_VERSION
@@ -97,8 +104,10 @@ def _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, 
     a.flags = (0 if clamp else nat.FLAG_NO_CLAMP) | (nat.FLAG_NAN_ZERO_U if nan_policy == "zero_u" else 0)
     a.B, a.S, a.H, a.hd, a.K = B, S, H, hd, K
     a.x, a.x_dtype, a.x_stride_b, a.x_stride_s = x.data_ptr(), _dtype_code(x.dtype), x.stride(0), x.stride(1)
-    a.out, a.out_dtype = out.data_ptr(), _dtype_code(out.dtype)
-    a.out_stride_b, a.out_stride_s = out.stride(0), out.stride(1)
+    a.out_dtype = _dtype_code(odt)
+    if out is not None:
+        a.out = out.data_ptr()
+        a.out_stride_b, a.out_stride_s = out.stride(0), out.stride(1)
     a.coeffs, a.c_stride_b, a.c_stride_h, a.c_stride_k = c.data_ptr(), c.stride(0), c.stride(1), c.stride(2)
     a.damping, a.lam = damp.data_ptr(), lamt.data_ptr()
     if gt is not None:
@@ -135,7 +144,7 @@ def cheby_ema_forward(x: torch.Tensor, coeffs: torch.Tensor, damping: Sequence[f
     nbytes = lib.osm_workspace_bytes(ctypes.byref(a), 0)
     if nbytes == 0:
         nat.check(_rc_from_error(lib, a, 0))
-    ws = _workspace(dev, stream, nbytes)
+    ws = _workspace(dev, stream, nbytes, nat.OP_FWD)
     nat.check(lib.osm_cheby_ema_fwd(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
                                     ctypes.c_void_p(stream)))
     del keep
@@ -170,11 +179,125 @@ def cheby_ema_ttt(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, *, g: tor
     nbytes = lib.osm_workspace_bytes(ctypes.byref(a), 1)
     if nbytes == 0:
         nat.check(_rc_from_error(lib, a, 1))
-    ws = _workspace(dev, stream, nbytes)
+    ws = _workspace(dev, stream, nbytes, nat.OP_TTT)
     nat.check(lib.osm_cheby_ema_ttt(ctypes.byref(a), ctypes.c_void_p(grad.data_ptr()), tgt,
                                     ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(stream)))
     del keep
     return (out, grad, ema_final) if return_state else (out, grad)
+
+
+def cheby_ema_backward(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, out: torch.Tensor | None,
+                       grad_out: torch.Tensor, *, g: torch.Tensor | None = None, lam_shift: float = 0.004,
+                       lam_min: float = 0.9, lam_max: float = 0.9999, grad_state: torch.Tensor | None = None,
+                       clamp: bool = True, nan_policy: str = "zero_z", need_coeffs: bool = True,
+                       need_init: bool = False, grad_x_out: torch.Tensor | None = None,
+                       grad_coeffs_out: torch.Tensor | None = None, grad_init_out: torch.Tensor | None = None):
+    """Backward of ``cheby_ema_forward``.
+
+    ``out`` is the saved forward output (its clamp mask |out| < 1 - 1e-6
+    gates the adjoint, as the reference's reverse scan does; it may be None
+    with clamp=False), ``grad_out`` = dL/dout [B,S,D] and ``grad_state`` =
+    dL/d ema_final [B,D] or None.  Returns (grad_x [B,S,D] in x's dtype,
+    grad_coeffs [B,H,K,hd] fp32 or None, grad_init [B,D] fp32 or None).
+    lambda and damping are treated as constants.  ``grad_x_out``,
+    ``grad_coeffs_out`` and ``grad_init_out`` (contiguous, on the device)
+    receive the results instead of new tensors.
+    """
+    lib = nat.load()
+    if out is None and clamp:
+        raise ValueError("the saved forward output is needed for the clamp mask")
+    a, _, keep = _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, None, clamp,
+                          out.dtype if out is not None else None, out, nan_policy, alloc_out=False)
+    xin = keep[0]
+    dev = xin.device
+    B, S, D = a.B, a.S, a.H * a.hd
+    out_dt = out.dtype if out is not None else xin.dtype
+    go = grad_out.to(device=dev, dtype=out_dt)
+    if tuple(go.shape) != (B, S, D):
+        raise ValueError(f"grad_out must be [B,S,D]=({B},{S},{D}), got {tuple(grad_out.shape)}")
+    if go.stride(2) != 1 or go.stride(1) % 4 or go.stride(0) % 4 or go.data_ptr() % (4 * go.element_size()):
+        go = go.contiguous()
+    if grad_x_out is None:
+        gx = torch.empty((B, S, D), device=dev, dtype=xin.dtype)
+    else:
+        if tuple(grad_x_out.shape) != (B, S, D) or grad_x_out.dtype != xin.dtype or \
+                grad_x_out.device != dev or not grad_x_out.is_contiguous():
+            raise ValueError(f"grad_x_out must be a contiguous {xin.dtype} tensor of shape {(B, S, D)} on {dev}")
+        gx = grad_x_out
+    gc = gi = None
+    if grad_coeffs_out is not None:
+        _check_dest(grad_coeffs_out, (B, a.H, a.K, a.hd), dev, "grad_coeffs_out")
+        gc = grad_coeffs_out
+    elif need_coeffs:
+        gc = torch.empty((B, a.H, a.K, a.hd), device=dev, dtype=torch.float32)
+    if grad_init_out is not None:
+        _check_dest(grad_init_out, (B, D), dev, "grad_init_out")
+        gi = grad_init_out
+    elif need_init:
+        gi = torch.empty((B, D), device=dev, dtype=torch.float32)
+    gs = None
+    if grad_state is not None:
+        gs = grad_state.to(device=dev, dtype=torch.float32).reshape(B, D).contiguous()
+    bw = nat.BwdArgs()
+    bw.grad_out, bw.go_stride_b, bw.go_stride_s = go.data_ptr(), go.stride(0), go.stride(1)
+    bw.grad_state = gs.data_ptr() if gs is not None else None
+    bw.grad_x, bw.gx_stride_b, bw.gx_stride_s = gx.data_ptr(), gx.stride(0), gx.stride(1)
+    bw.grad_coeffs = gc.data_ptr() if gc is not None else None
+    bw.grad_init = gi.data_ptr() if gi is not None else None
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    nbytes = lib.osm_workspace_bytes(ctypes.byref(a), nat.OP_BWD)
+    if nbytes == 0:
+        nat.check(lib.osm_cheby_ema_bwd(ctypes.byref(a), ctypes.byref(bw), None, 0, None))
+    ws = _workspace(dev, stream, nbytes, nat.OP_BWD)
+    nat.check(lib.osm_cheby_ema_bwd(ctypes.byref(a), ctypes.byref(bw), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                    ctypes.c_void_p(stream)))
+    del keep, go, gs
+    return gx, gc, gi
+
+
+class _ChebyEMAFunction(torch.autograd.Function):
+    """Differentiable forward: saves x, coeffs and the output; the backward
+    is one ``osm_cheby_ema_bwd`` call."""
+
+    @staticmethod
+    def forward(ctx, x, coeffs, ema_init, damping, lam, g, lam_shift, lam_min, lam_max, clamp, out_dtype,
+                nan_policy):
+        out, fin = cheby_ema_forward(x, coeffs, damping, lam, g=g, lam_shift=lam_shift, lam_min=lam_min,
+                                     lam_max=lam_max, ema_init=ema_init, clamp=clamp, out_dtype=out_dtype,
+                                     return_state=True, nan_policy=nan_policy)
+        ctx.save_for_backward(x, coeffs, out if clamp else None, g)
+        ctx.params = (damping, lam, lam_shift, lam_min, lam_max, clamp, nan_policy)
+        ctx.has_init = ema_init is not None
+        return out, fin
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_fin):
+        x, coeffs, out, g = ctx.saved_tensors
+        damping, lam, lam_shift, lam_min, lam_max, clamp, nan_policy = ctx.params
+        need_x, need_c, need_i = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
+        if grad_out is None:
+            grad_out = torch.zeros(x.shape, device=x.device, dtype=out.dtype if out is not None else x.dtype)
+        gx, gc, gi = cheby_ema_backward(x, coeffs, damping, lam, out, grad_out, g=g, lam_shift=lam_shift,
+                                        lam_min=lam_min, lam_max=lam_max, grad_state=grad_fin, clamp=clamp,
+                                        nan_policy=nan_policy, need_coeffs=need_c, need_init=need_i)
+        if need_x and gx.dtype != x.dtype:
+            gx = gx.to(x.dtype)
+        if need_c and gc.dtype != coeffs.dtype:
+            gc = gc.to(coeffs.dtype)
+        return (gx if need_x else None, gc, gi if ctx.has_init else None,
+                None, None, None, None, None, None, None, None, None)
+
+
+def cheby_ema(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, *, g: torch.Tensor | None = None,
+              lam_shift: float = 0.004, lam_min: float = 0.9, lam_max: float = 0.9999,
+              ema_init: torch.Tensor | None = None, clamp: bool = True, out_dtype: torch.dtype | None = None,
+              return_state: bool = False, nan_policy: str = "zero_z"):
+    """``cheby_ema_forward`` as a differentiable op: gradients flow to x,
+    coeffs and ema_init (lambda, g and damping are constants).  Returns out,
+    or (out, ema_final) when return_state."""
+    out, fin = _ChebyEMAFunction.apply(x, coeffs, ema_init, damping, lam, g, lam_shift, lam_min, lam_max, clamp,
+                                       out_dtype, nan_policy)
+    return (out, fin) if return_state else out
 
 
 def _check_dest(t: torch.Tensor, shape, dev, name: str) -> None:

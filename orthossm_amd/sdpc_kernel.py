@@ -11,17 +11,20 @@ NaN input counted as u = 0 as that path does (sdpc_kernel.py:1725); the
 coefficients and momentum come back unchanged (cast to fp32, as
 sdpc_kernel.py:2549-2552).  The Chebyshev series is evaluated exactly
 (the reference's fast path also evaluates it exactly, by basis + einsum).
+Gradients flow to x and coeffs through the fused backward, as the
+reference's autograd does through that path (its EMA backward
+_EMAFastPathFn.backward, sdpc_kernel.py:1677-1701, masks the adjoint with
+|out| < 1 - 1e-6).
 
 Not covered yet: the full path with online Lion TTT over 256-token chunks
-(``FusedChebyRKVv10``, sdpc_kernel.py:2351-2515) and gradients through the
-op.  Both raise ``NotImplementedError`` instead of silently changing
-semantics.
+(``FusedChebyRKVv10``, sdpc_kernel.py:2351-2515).  It raises
+``NotImplementedError`` instead of silently changing semantics.
 """
 from __future__ import annotations
 
 import torch
 
-from .ops import cheby_ema_forward
+from .ops import cheby_ema, cheby_ema_forward
 
 
 def v10_damping(n_heads: int, device=None) -> torch.Tensor:
@@ -46,14 +49,15 @@ def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_m
             "orthossm_amd: the full path (online Lion TTT over chunks, S >= seq_threshold) is not "
             "implemented; call with seq_threshold > S for the fixed-coefficient path, or use "
             "orthossm_amd.cheby_ema_ttt for the fused TTT gradient.")
-    if torch.is_grad_enabled() and (x.requires_grad or coeffs.requires_grad):
-        raise NotImplementedError("orthossm_amd: gradients through apply_cheby_rkv_v10 are not implemented")
     H = n_heads
     if D % H:
         raise ValueError(f"D={D} is not divisible by n_heads={H}")
     damping = v10_damping(H, x.device)
     lam = torch.full((H,), float(ema_momentum), dtype=torch.float32, device=x.device)
-    out = cheby_ema_forward(x, coeffs, damping, lam, out_dtype=torch.float32, nan_policy="zero_u")
+    if torch.is_grad_enabled() and (x.requires_grad or coeffs.requires_grad):
+        out = cheby_ema(x, coeffs, damping, lam, out_dtype=torch.float32, nan_policy="zero_u")
+    else:
+        out = cheby_ema_forward(x, coeffs, damping, lam, out_dtype=torch.float32, nan_policy="zero_u")
     return out, coeffs, momentum_buf
 
 

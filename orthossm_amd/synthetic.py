@@ -26,6 +26,7 @@ class Config:
     dtype: torch.dtype = torch.float32
     ttt: bool = False
     chunk: int = 0  # >0: processed as consecutive chunks with EMA carry
+    bwd: bool = False  # the backward pass (dL/dx, dL/dc, dL/d ema_init) instead of the forward
 
     @property
     def hd(self) -> int:
@@ -39,6 +40,8 @@ CONFIGS = {
     "streaming": Config("streaming", B=1, S=262144, D=512, H=8, chunk=16384),
     "dynamic": Config("dynamic", B=8, S=32768, D=1024, H=8, dynamic=True),
     "bf16_ttt": Config("bf16_ttt", B=16, S=65536, D=512, H=8, dtype=torch.bfloat16, ttt=True),
+    # the backward of configs[1]
+    "backward": Config("backward", B=4, S=16384, D=512, H=8, bwd=True),
 }
 
 

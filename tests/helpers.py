@@ -45,3 +45,21 @@ def oracle_ttt(inp, **kw):
     g = inp.get("g")
     return O.ttt_grad(inp["x"].double().numpy(), inp["coeffs"].numpy(), inp["damping"].numpy(),
                       inp["lam"].numpy(), g=None if g is None else g.numpy(), **kw)
+
+
+def oracle_backward(inp, grad_out, **kw):
+    g = inp.get("g")
+    return O.backward(inp["x"].double().numpy(), inp["coeffs"].numpy(), inp["damping"].numpy(),
+                      inp["lam"].numpy(), np.asarray(grad_out, dtype=np.float64),
+                      g=None if g is None else g.numpy(), **kw)
+
+
+# Gradient tolerance of the spec: 1e-3 relative.  Checked normalised by the
+# largest reference magnitude and elementwise with a floor of 1e-4 of it.
+GRAD_RTOL = 1e-3
+
+
+def assert_close_grad(got, want, rtol=GRAD_RTOL, what="grad"):
+    want = np.asarray(want, dtype=np.float64)
+    scale = float(np.max(np.abs(want))) if want.size else 0.0
+    assert_close_fp32(got, want, rtol=rtol, atol=1e-4 * scale + 1e-30, what=what)

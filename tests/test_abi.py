@@ -35,20 +35,22 @@ def test_every_declared_function_is_exported():
         assert hasattr(lib, name), name
 
 
-def test_struct_layout_matches_ctypes():
-    fields = [f for f, _ in nat.ChebyArgs._fields_]
+@pytest.mark.parametrize("cls,cname", [(nat.ChebyArgs, "osm_cheby_args"), (nat.BwdArgs, "osm_cheby_bwd_args")])
+def test_struct_layout_matches_ctypes(cls, cname):
+    fields = [f for f, _ in cls._fields_]
     prog = ['#include <stdio.h>', '#include <stddef.h>', '#include "osm.h"', "int main(void){",
-            'printf("%zu\\n", sizeof(osm_cheby_args));']
-    prog += [f'printf("%zu\\n", offsetof(osm_cheby_args, {f}));' for f in fields]
+            f'printf("%zu\\n", sizeof({cname}));']
+    prog += [f'printf("%zu\\n", offsetof({cname}, {f}));' for f in fields]
     prog += ["return 0;}"]
     with tempfile.TemporaryDirectory() as d:
         src, exe = os.path.join(d, "p.c"), os.path.join(d, "p")
         open(src, "w").write("\n".join(prog))
         subprocess.run(["gcc", "-std=c99", "-I", os.path.join(ROOT, "include"), src, "-o", exe], check=True)
         vals = [int(v) for v in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
-    assert vals[0] == ctypes.sizeof(nat.ChebyArgs)
+    assert vals[0] == ctypes.sizeof(cls)
+    assert len(vals) == len(fields) + 1
     for f, off in zip(fields, vals[1:]):
-        assert getattr(nat.ChebyArgs, f).offset == off, f
+        assert getattr(cls, f).offset == off, f
 
 
 def _args(**kw):
@@ -115,6 +117,47 @@ def test_ttt_argument_errors():
     assert lib.osm_cheby_ema_ttt(ctypes.byref(a), None, 0, None, 0, None) == -1        # grad NULL
     assert lib.osm_cheby_ema_ttt(ctypes.byref(a), ctypes.c_void_p(0x10000), 5, None, 0, None) == -1  # target
     assert lib.osm_workspace_bytes(ctypes.byref(a), 1) > lib.osm_workspace_bytes(ctypes.byref(a), 0)
+
+
+def test_bwd_workspace_bytes_formula():
+    lib = nat.load()
+    a = _args()
+    # 128-token tiles (n_tiles = 128 at S=16384), two look-back words per
+    # lane, then K-padded partials per tile and per chunk of 16 tiles.
+    slots = (2048 + 32 * 128 * 64 * 16 + 255) // 256 * 256
+    assert lib.osm_workspace_bytes(ctypes.byref(a), nat.OP_BWD) == slots + (32 * 128 + 32 * 8) * 8 * 64 * 4
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 3) == 0
+    assert b"osm_op" in lib.osm_last_error()
+
+
+def _bwd(**kw):
+    b = nat.BwdArgs()
+    b.grad_out = b.grad_x = 0x10000
+    b.go_stride_b = b.gx_stride_b = 16384 * 512
+    b.go_stride_s = b.gx_stride_s = 512
+    for k, v in kw.items():
+        setattr(b, k, v)
+    return b
+
+
+@pytest.mark.parametrize("akw,bkw,code", [
+    ({}, dict(grad_out=0), -1),
+    ({}, dict(grad_x=0), -1),
+    ({}, dict(grad_x=0x10004), -4),
+    ({}, dict(go_stride_s=510), -4),
+    ({}, dict(gx_stride_s=256), -4),          # rows overlap
+    ({}, dict(gx_stride_b=512), -4),          # batches overlap
+    (dict(out=0), {}, -1),                    # the clamp mask needs the saved output
+    (dict(out=0, flags=nat.FLAG_NO_CLAMP), {}, -5),   # ... unless there is no clamp: reaches the workspace check
+    (dict(K=9), {}, -2),
+])
+def test_bwd_argument_errors(akw, bkw, code):
+    lib = nat.load()
+    a = _args(**akw)
+    b = _bwd(**bkw)
+    assert lib.osm_cheby_ema_bwd(ctypes.byref(a), ctypes.byref(b), None, 0, None) == code
+    assert lib.osm_last_error() != b""
+    assert lib.osm_cheby_ema_bwd(ctypes.byref(_args()), None, None, 0, None) == -1
 
 
 def test_error_messages_are_thread_local():

@@ -1,5 +1,6 @@
 """Host-side behaviour of the drop-in apply_cheby_rkv_v10 that needs no GPU:
-the paths it does not implement raise instead of changing semantics."""
+the paths it does not implement raise instead of changing semantics, and
+CPU tensors raise (there is no CPU path)."""
 import pytest
 import torch
 
@@ -19,10 +20,10 @@ def test_full_path_raises():
         apply_cheby_rkv_v10(x, c, None, n_heads=4, seq_threshold=0)
 
 
-def test_gradients_raise():
+def test_gradient_path_is_gpu_only_too():
     x = torch.zeros(1, 16, 64, requires_grad=True)
-    c = torch.zeros(1, 4, 4, 16)
-    with pytest.raises(NotImplementedError):
+    c = torch.zeros(1, 4, 4, 16, requires_grad=True)
+    with pytest.raises(RuntimeError, match="ROCm GPU only"):
         apply_cheby_rkv_v10(x, c, None, n_heads=4)
 
 

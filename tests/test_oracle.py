@@ -362,6 +362,26 @@ def test_reference_form_agrees_with_oracle():
     assert O.rel_err(fin_rf.numpy(), fin_u) < 2e-6
 
 
+def test_reference_form_backward_agrees_with_oracle():
+    B, S, H, hd, K = 2, 150, 4, 8, 8
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn(B, S, H * hd, generator=gen)
+    x[0, 5, 3] = float("nan")
+    x[1, 9, 0] = 0.0
+    c = torch.randn(B, H, K, hd, generator=gen) / torch.arange(1, K + 1).view(1, 1, K, 1)
+    c[1, 2, 0, :] = 12.0                     # head 2 of batch 1 saturates: the mask binds
+    damp = torch.tensor([0.9 ** h for h in range(H)])
+    lam = torch.tensor([0.9995, 0.997, 0.8, 0.95])
+    go = torch.randn(B, S, H * hd, generator=gen)
+    out_rf, _ = RF.forward(x, c, damp, lam, ema_init=None)
+    gx_rf, gc_rf = RF.backward(x, c, damp, lam, out_rf, go)
+    assert (out_rf.abs() >= 1 - 1e-6).any()
+    gx, gc, _ = O.backward(x.numpy(), c.numpy(), damp.numpy(), lam.numpy(), go.double().numpy(),
+                           nan_policy="zero_u", out_saved=out_rf.numpy())
+    assert O.rel_err(gx_rf.numpy(), gx) < 2e-5
+    assert O.rel_err(gc_rf.numpy(), gc) < 2e-5
+
+
 # ---------------------------------------------------------------- mutation checks
 def test_pins_catch_a_dropped_coefficient(monkeypatch):
     """The reference's megakernel Clenshaw fallback drops c4..c7
