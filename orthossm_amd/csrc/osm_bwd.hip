@@ -32,8 +32,8 @@
 //   4. pass 2, last token first: a, e, dL/dx stored, sum_t e T_k(u) kept in
 //      registers;
 //   5. the tile's sums over its runs -> partials[lane-block][tile][k][lane].
-// Two small kernels add the partials over tiles in a fixed order (results do
-// not depend on timing) and scale them into dL/dc.
+// A small kernel adds the partials over tiles in a fixed order (results do
+// not depend on timing) and scales them into dL/dc.
 #include "osm_tile.h"
 
 namespace osm {
@@ -42,7 +42,6 @@ namespace {
 constexpr float kMaskBound = 0.999999f;         // 1 - 1e-6 rounded to fp32, as the reference compares in fp32
 constexpr float kSoftsignGradMin = 1e-7f;       // the reference's clamp of |x| in the softsign
 constexpr float kTwoLn2 = 1.3862943611198906f;  // dL/dx from y' = 2 log2(e) damping p'
-constexpr int kBwdChunk = 16;                   // tiles summed per thread by the first reduction
 
 // One [B,S,*] tensor's rows of a tile: descriptor from the tile's first row
 // to the end of row S-1, per-thread lane offset, uniform step per token.
@@ -303,34 +302,35 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
   finish_block(p.hdr, tags.epoch);
 }
 
-// Level 1: thread (k, lane) adds up to kBwdChunk consecutive tiles.
-template <int KP>
-__global__ void __launch_bounds__(KP * kLanes) bwd_sum_chunks(const float* partials, float* chunks, int n_tiles,
-                                                              int n_chunks) {
-  const int chunk = blockIdx.x, lb = blockIdx.y, i = threadIdx.x;
-  const int first = chunk * kBwdChunk;
-  const int end = min(first + kBwdChunk, n_tiles);
-  float acc = 0.0f;
-  for (int t = first; t < end; ++t) acc += partials[((size_t)lb * n_tiles + t) * KP * kLanes + i];
-  chunks[((size_t)lb * n_chunks + chunk) * KP * kLanes + i] = acc;
-}
+// dL/dc[b,h,k,j] = 4 damping_h (1 - lam_h if static) * sum over the tiles of
+// lane-block lb.  Block (k, lb): slice sl of kRedSlices adds tiles sl,
+// sl + kRedSlices, ... of each lane, then the slices are added in order, so
+// the result does not depend on timing.
+constexpr int kRedSlices = 16;
 
-// Level 2: add the chunks in order and write
-// dL/dc[b,h,k,j] = 4 damping_h (1 - lam_h if static) * sum.
 template <int KP>
-__global__ void __launch_bounds__(KP * kLanes) bwd_finalize(const float* chunks, float* grad, const float* damping,
-                                                            const float* lam, int dyn, int n_chunks, int n_lbd, int D,
-                                                            int hd, int H, int K) {
-  const int lb = blockIdx.x, i = threadIdx.x;
-  const int k = i / kLanes, l = i - k * kLanes;
+__global__ void __launch_bounds__(kRedSlices * kLanes) bwd_reduce(const float* partials, float* grad,
+                                                                 const float* damping, const float* lam, int dyn,
+                                                                 int n_tiles, int n_lbd, int D, int hd, int H, int K) {
+  __shared__ float red[kRedSlices][kLanes];
+  const int k = blockIdx.x, lb = blockIdx.y;
+  const int sl = threadIdx.x / kLanes, l = threadIdx.x - sl * kLanes;
+  const float* src = partials + (size_t)lb * n_tiles * KP * kLanes + (size_t)k * kLanes + l;
   float acc = 0.0f;
-  for (int c = 0; c < n_chunks; ++c) acc += chunks[((size_t)lb * n_chunks + c) * KP * kLanes + i];
+#pragma unroll 8
+  for (int t = sl; t < n_tiles; t += kRedSlices) acc += src[(size_t)t * KP * kLanes];
+  red[sl][l] = acc;
+  __syncthreads();
+  if (sl != 0) return;
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kRedSlices; ++i) sum += red[i][l];
   const int b = lb / n_lbd;
   const int d = (lb - b * n_lbd) * kLanes + l;
   if (d >= D || k >= K) return;
   const int h = d / hd, j = d - h * hd;
   const float scale = 4.0f * damping[h] * (dyn ? 1.0f : 1.0f - lam[h]);
-  grad[(((size_t)b * H + h) * K + k) * hd + j] = acc * scale;
+  grad[(((size_t)b * H + h) * K + k) * hd + j] = sum * scale;
 }
 
 template <class G, bool DYN, typename XT, typename OT, int KP>
@@ -340,14 +340,8 @@ hipError_t launch_all(const BwdParams& bp, hipStream_t stream) {
   hipLaunchKernelGGL((cheby_ema_bwd_kernel<G, DYN, XT, OT, KP>), dim3(grid), dim3(G::THREADS), 0, stream, bp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !bp.grad_coeffs) return e;
-  const int n_chunks = (p.n_tiles + kBwdChunk - 1) / kBwdChunk;
-  float* chunks = p.partials + (size_t)p.n_lb * p.n_tiles * KP * kLanes;
-  hipLaunchKernelGGL((bwd_sum_chunks<KP>), dim3(n_chunks, p.n_lb), dim3(KP * kLanes), 0, stream, p.partials, chunks,
-                     p.n_tiles, n_chunks);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((bwd_finalize<KP>), dim3(p.n_lb), dim3(KP * kLanes), 0, stream, chunks, bp.grad_coeffs,
-                     p.damping, p.lam, DYN ? 1 : 0, n_chunks, p.n_lbd, p.D, p.hd, p.H, p.K);
+  hipLaunchKernelGGL((bwd_reduce<KP>), dim3(KP, p.n_lb), dim3(kRedSlices * kLanes), 0, stream, p.partials,
+                     bp.grad_coeffs, p.damping, p.lam, DYN ? 1 : 0, p.n_tiles, p.n_lbd, p.D, p.hd, p.H, p.K);
   return hipGetLastError();
 }
 
@@ -375,9 +369,8 @@ size_t bwd_slot_bytes(int n_lb, int n_tiles) { return fwd_workspace_bytes(n_lb, 
 
 size_t bwd_workspace_bytes(int n_lb, int n_tiles, int K) {
   const size_t kpad = K <= 4 ? 4 : 8;
-  const size_t n_chunks = (n_tiles + kBwdChunk - 1) / kBwdChunk;
   const size_t slots = (bwd_slot_bytes(n_lb, n_tiles) + 255) / 256 * 256;
-  return slots + ((size_t)n_lb * n_tiles + (size_t)n_lb * n_chunks) * kpad * kLanes * sizeof(float);
+  return slots + (size_t)n_lb * n_tiles * kpad * kLanes * sizeof(float);
 }
 
 hipError_t launch_bwd(const BwdParams& p, int x_dtype, int out_dtype, bool dyn, int tile, int kpad,

@@ -18,7 +18,7 @@ namespace osm {
 // (runs) are ordered wave-major: tg = wave * TGW + lane_in_wave / TPR.  The
 // look-back serves each 64-lane sub-block with WPS waves of WPT words per
 // thread, so tiles are grouped in checkpoint runs of CKPT = WPS * WPT.
-template <int LPT_, int WAVES_, int R_, int LANES_ = 64>
+template <int LPT_, int WAVES_, int R_, int LANES_ = 64, int WPT_ = 8>
 struct TileGeo {
   static constexpr int LPT = LPT_;            // lanes per thread
   static constexpr int WAVES = WAVES_;        // waves per workgroup
@@ -31,7 +31,7 @@ struct TileGeo {
   static constexpr int NTG = WAVES * TGW;     // token groups per tile
   static constexpr int TILE = NTG * R;        // tokens per tile
   static constexpr int WPS = WAVES / NSUB;    // look-back waves per sub-block
-  static constexpr int WPT = 8;               // look-back words per thread
+  static constexpr int WPT = WPT_;            // look-back words per thread
   static constexpr int CKPT = WPS * WPT;      // checkpoint interval, tiles
   static_assert(LANES % 64 == 0 && LANES % LPT == 0 && TPR <= 64 && 64 % TPR == 0, "geometry");
   static_assert(WAVES % NSUB == 0, "look-back waves");
@@ -66,9 +66,13 @@ int ttt_tile_tokens(bool dyn, int x_dtype);
 
 // Backward: one lane per thread (the clamp mask makes the adjoint map's A
 // differ per lane); x and dL/dout of the run stay in registers between the
-// passes (plus lambda per token with a dynamic lambda).  32-token runs
-// spill at 128 VGPRs; 16-token runs fit in ~100 (static) and ~117 (dynamic).
-using BwdTile = TileGeo<1, 8, 16>;   // 128 tokens
+// passes (plus lambda per token with a dynamic lambda), and the look-back
+// reads two words (A, B) per predecessor.  Four look-back words per thread
+// (checkpoints every 32 tiles) instead of eight bring the static kernel from
+// 101 to 77 VGPRs, three workgroups per CU instead of two: 129 against 141 us
+// at BASELINE configs[1] on MI355X.  32-token runs spill; 8-token runs are
+// slower (185 us).
+using BwdTile = TileGeo<1, 8, 16, 64, 4>;   // 128 tokens
 int bwd_tile_tokens(bool dyn);
 
 // Workspace: a kHeaderBytes header (launch epoch, fault word, completion

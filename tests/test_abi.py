@@ -123,9 +123,9 @@ def test_bwd_workspace_bytes_formula():
     lib = nat.load()
     a = _args()
     # 128-token tiles (n_tiles = 128 at S=16384), two look-back words per
-    # lane, then K-padded partials per tile and per chunk of 16 tiles.
+    # lane, then K-padded partials per tile.
     slots = (2048 + 32 * 128 * 64 * 16 + 255) // 256 * 256
-    assert lib.osm_workspace_bytes(ctypes.byref(a), nat.OP_BWD) == slots + (32 * 128 + 32 * 8) * 8 * 64 * 4
+    assert lib.osm_workspace_bytes(ctypes.byref(a), nat.OP_BWD) == slots + 32 * 128 * 8 * 64 * 4
     assert lib.osm_workspace_bytes(ctypes.byref(a), 3) == 0
     assert b"osm_op" in lib.osm_last_error()
 
