@@ -1,0 +1,179 @@
+"""Pins of the full-path oracle (oracle/v10_full.py) against library
+routines, closed forms and brute force (CPU only)."""
+import math
+
+import numpy as np
+import pytest
+import scipy.signal
+import torch
+from numpy.polynomial import chebyshev as npcheb
+
+from oracle import v10_full as V
+
+rng = np.random.default_rng(4321)
+
+
+def test_bf16_round_matches_torch():
+    x = rng.standard_normal(20000).astype(np.float32) * 10 ** rng.uniform(-40, 38, 20000).astype(np.float32)
+    x[:6] = [0.0, -0.0, np.inf, -np.inf, 3.3895314e38, 1e-45]
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    got = V.bf16_round(x)
+    np.testing.assert_array_equal(got, want.astype(np.float64))
+    assert np.isnan(V.bf16_round(np.array([np.nan], np.float32)))[0]
+
+
+def test_lut_is_chebyshev_at_its_grid():
+    lut = V.chebyshev_lut()
+    grid = torch.linspace(0.0, 1.0, 256).numpy().astype(np.float64)
+    for k in range(8):
+        np.testing.assert_allclose(lut[k], np.cos(k * np.arccos(grid)), atol=2e-6)
+
+
+@pytest.mark.parametrize("K", [1, 3, 8])
+def test_lut_series_interpolates_the_chebyshev_series(K):
+    lut = V.chebyshev_lut()
+    c = rng.standard_normal((40, K))
+    # at the grid points (both signs, odd terms flip): the series itself
+    i = rng.integers(0, 256, 40)
+    a = i / 255.0
+    for sgn in (1.0, -1.0):
+        got = V.lut_series(c, a, np.full(40, sgn), lut)
+        want = np.array([npcheb.chebval(sgn * a[j], c[j]) for j in range(40)])
+        np.testing.assert_allclose(got, want, atol=2e-5 * K)
+    # between grid points: linear interpolation error <= h^2/8 max|p''|
+    a = rng.uniform(0, 1, 40)
+    got = V.lut_series(c, a, np.ones(40), lut)
+    want = np.array([npcheb.chebval(a[j], c[j]) for j in range(40)])
+    bound = (1 / 255) ** 2 / 8 * np.abs(c).sum(axis=1) * (K - 1) ** 4 + 2e-5 * K
+    assert np.all(np.abs(got - want) <= bound)
+
+
+def test_clenshaw4_uses_only_the_first_four_coefficients():
+    c = rng.standard_normal((30, 8))
+    u = rng.uniform(-1, 1, 30)
+    got = V.clenshaw4_series(c, u)
+    want = np.array([npcheb.chebval(u[j], c[j, :4]) for j in range(30)])
+    np.testing.assert_allclose(got, want, rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(V.clenshaw4_series(c[:, :2], u),
+                               [npcheb.chebval(u[j], c[j, :2]) for j in range(30)], atol=1e-13)
+
+
+def test_softsign_special_values():
+    xb = np.array([np.nan, 0.0, -0.0, 1.0, -3.0, np.inf, -np.inf])
+    u, absu, sign, nan = V.v10_softsign(xb)
+    assert nan.tolist() == [True] + [False] * 6
+    assert u[0] > 0 and u[0] == u[1] == u[2] and u[0] < 1.2e-7          # NaN and +-0 -> +1e-7 side
+    np.testing.assert_allclose(u[3:], [0.5, -0.75, 1.0, -1.0], rtol=1e-12)
+
+
+def _chunk_inputs(B=2, L=40, H=2, hd=4, K=8):
+    x = V.bf16_round(rng.standard_normal((B, L, H * hd)).astype(np.float32))
+    c = rng.standard_normal((B, H, K, hd)) / np.arange(1, K + 1).reshape(1, 1, K, 1)
+    m = rng.standard_normal((B, H, K, hd)) * 0.01
+    return x, c, m
+
+
+KW = dict(ema_momentum=0.9, base_lr=0.005, beta1=0.9, beta2=0.99, wd=0.01)
+
+
+def test_chunk_ema_restarts_from_zero_and_matches_lfilter():
+    x, c, m = _chunk_inputs()
+    s, _, _, z = V.v10_chunk(x, c, m, **KW)
+    for b in range(2):
+        for d in range(8):
+            y = scipy.signal.lfilter([0.1], [1, -0.9], z[b, :, d])
+            np.testing.assert_allclose(s[b, :, d], y, rtol=1e-12, atol=1e-15)
+    assert np.all(np.abs(z) <= math.tanh(4.0) + 1e-15)
+
+
+def test_chunk_tanh_clamps_at_four_and_nan_gives_zero():
+    x, c, m = _chunk_inputs(B=1, L=6, H=1, hd=4, K=2)
+    c[0, 0, 0, :] = [50.0, -50.0, 0.2, 0.0]
+    c[0, 0, 1, :] = 0.0
+    x[0, 3, 2] = np.nan
+    _, _, _, z = V.v10_chunk(x, c, m, **KW)
+    gamma = 0.98
+    np.testing.assert_allclose(z[0, :, 0], math.tanh(4.0), rtol=1e-14)
+    np.testing.assert_allclose(z[0, :, 1], -math.tanh(4.0), rtol=1e-14)
+    np.testing.assert_allclose(z[0, [0, 1, 2, 4, 5], 2], math.tanh(0.2 * gamma), rtol=1e-13)
+    assert z[0, 3, 2] == 0.0
+
+
+def test_proxy_gradient_brute_force():
+    B, L, D, K = 1, 9, 3, 8
+    u = rng.uniform(-1, 1, (B, L, D))
+    s = rng.uniform(-1, 1, (B, L, D))
+    got = V.proxy_grad(u, s, K)
+    for d in range(D):
+        for k in range(K):
+            acc = 0.0
+            for t in range(L - 1):
+                e = u[0, t + 1, d] - s[0, t, d]
+                acc += e / (1 + math.exp(-3 * abs(e))) * math.cos(k * math.acos(u[0, t, d]))
+            assert got[0, d, k] == pytest.approx(acc, rel=1e-10, abs=1e-12)
+    # s that predicts u one step ahead gives no gradient
+    s2 = np.zeros_like(s)
+    s2[:, :-1] = u[:, 1:]
+    assert np.all(V.proxy_grad(u, s2, K) == 0)
+
+
+def test_lion_closed_forms():
+    B, H, K, hd = 2, 4, 3, 1
+    c = np.ones((B, H, K, hd))
+    m = np.zeros((B, H, K, hd))
+    gc = np.zeros((B, H, K, hd))
+    gc[0, :, 0] = 5.0            # g = +1 over L = 6 tokens
+    gc[0, :, 1] = -5.0
+    gc[1, 0, 2] = 1e-30
+    cn, mn = V.lion_update(c, m, gc, 6, base_lr=0.005, beta1=0.9, beta2=0.99, wd=0.01)
+    lam = np.array([0.9995, 0.9995, 0.997, 0.997])
+    lr = 0.005 * (1 + 0.25 * (np.arange(4) - 2) / 4)
+    decay = lam - lr * 0.01
+    np.testing.assert_allclose(cn[0, :, 0, 0], decay + lr, rtol=1e-14)                 # sign +1, ss_0 = 1
+    np.testing.assert_allclose(cn[0, :, 1, 0], decay - lr / 2 ** 1.5, rtol=1e-14)      # sign -1, ss_1
+    np.testing.assert_allclose(cn[0, :, 2, 0], decay, rtol=1e-14)                      # g = 0: sign 0
+    np.testing.assert_allclose(mn[0, :, 0, 0], 0.01, rtol=1e-12)                       # (1 - b2) g
+    assert cn[1, 0, 2, 0] == pytest.approx(decay[0] + lr[0] / 3 ** 1.5, rel=1e-14)
+    # gate scales lr (and so the decay); dynamic lambda moves the forget factor
+    gate = np.array([0.5, 2.0])
+    dyn = np.array([1.0, -50.0])
+    cg, _ = V.lion_update(c, m, gc, 6, base_lr=0.005, beta1=0.9, beta2=0.99, wd=0.01, gate=gate, dyn=dyn)
+    lam_d = np.minimum(lam + 0.008 * 0.5, 0.9999)
+    np.testing.assert_allclose(cg[0, :, 0, 0], lam_d - 0.5 * lr * 0.01 + 0.5 * lr, rtol=1e-14)
+    np.testing.assert_allclose(cg[1, :, 1, 0], 0.9 - 2 * lr * 0.01, rtol=1e-14)      # clamped at 0.9
+    # momentum drives the sign: m > 0 overrides a small negative g
+    m2 = np.full((B, H, K, hd), 1.0)
+    cm, mm = V.lion_update(c, m2, -gc * 1e-3, 6, base_lr=0.005, beta1=0.9, beta2=0.99, wd=0.01)
+    np.testing.assert_allclose(cm[0, :, 0, 0], decay + lr, rtol=1e-14)
+
+
+def test_lion_one_token_chunk_poisons_momentum_like_the_reference():
+    # len - 1 = 0: g = 0 * inf = NaN, so sign = 0 and momentum becomes NaN.
+    c = np.ones((1, 1, 2, 1))
+    cn, mn = V.lion_update(c, np.zeros_like(c), np.zeros_like(c), 1, base_lr=0.005, beta1=0.9, beta2=0.99,
+                           wd=0.01)
+    assert np.all(np.isnan(mn)) and np.all(np.isfinite(cn))
+
+
+def test_full_path_chains_coefficients_over_chunks():
+    B, S, H, hd, K = 2, 70, 2, 4, 8
+    x = rng.standard_normal((B, S, H * hd)).astype(np.float32)
+    c = rng.standard_normal((B, H, K, hd)) / np.arange(1, K + 1).reshape(1, 1, K, 1)
+    m = np.zeros_like(c)
+    out, cn, mn = V.v10_full(x, c, m, n_heads=H, chunk_size=32)
+    xb = V.bf16_round(x)
+    cc, mm = c, m
+    outs = []
+    for t0 in (0, 32, 64):
+        s, cc, mm, _ = V.v10_chunk(xb[:, t0:t0 + 32], cc, mm, **KW)
+        outs.append(V.bf16_round(s.astype(np.float32)))
+    np.testing.assert_array_equal(out, np.concatenate(outs, axis=1))
+    np.testing.assert_array_equal(cn, cc)
+    # the EMA restarts at every chunk: out at a chunk's first token is (1 - mu) z
+    _, _, _, z = V.v10_chunk(xb[:, 32:64], V.v10_chunk(xb[:, :32], c, m, **KW)[1],
+                             V.v10_chunk(xb[:, :32], c, m, **KW)[2], **KW)
+    np.testing.assert_allclose(out[:, 32], V.bf16_round((0.1 * z[:, 0]).astype(np.float32)))
+    # one chunk when S <= chunk_size
+    o1, c1, _ = V.v10_full(x[:, :20], c, m, n_heads=H, chunk_size=32)
+    s1, c1b, _, _ = V.v10_chunk(xb[:, :20], c, m, **KW)
+    np.testing.assert_array_equal(c1, c1b)
