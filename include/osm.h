@@ -142,6 +142,58 @@ typedef struct osm_cheby_bwd_args {
   float* grad_init;         /* optional [B, H*hd] fp32 contiguous: dL/d ema_init */
 } osm_cheby_bwd_args;
 
+/*
+ * The reference's full apply_cheby_rkv_v10 path (S >= seq_threshold): the
+ * sequence is cut into chunks of `chunk` tokens; each chunk runs with the
+ * current coefficients c and Lion momentum m, per lane:
+ *
+ *   u = sign(x)(1 - 1/(1 + max(|x|, 1e-7)))   on bf16(x); NaN reads as 0, sign(0) = +1
+ *   y = LUT(u) (OSM_V10_USE_LUT: 256-point half table `lut`, linear
+ *       interpolation, odd terms times sign(u)) or the 4-term Clenshaw c0..c3
+ *   z = tanh(clamp((0.98 - 0.06 h/H) y, -4, 4))   (0 for NaN x)
+ *   s = mu s + (1 - mu) z from s = 0 at the chunk start;  out = bf16(s) as fp32
+ *   gc_k = sum_{t, t+1 in chunk} gv T_k(u_t),  gv = err/(1 + exp(-3|err|)),
+ *          err = u_{t+1} - s_t
+ *   Lion: g = gc/(L-1); interp = b1 m + (1-b1) g; m <- b2 m + (1-b2) g;
+ *         c <- (lam_h - lr wd) c + lr ss_k sign(interp),
+ *         lr = base_lr lr_scale[h] (x gate[b]),
+ *         lam_h = lion_lambda[h] (or clamp(lam_h + 0.008 (dyn[b] - 0.5), 0.9, 0.9999))
+ *
+ * and the next chunk uses the updated (c, m).  Replaces the chunk loop of
+ * apply_cheby_rkv_v10 (sdpc_kernel.py:2574-2606) with its per-chunk
+ * FusedChebyRKVv10.forward / _launch_ortho_megakernel (2353-2433,
+ * 2290-2344).  One launch, no workspace.
+ */
+#define OSM_V10_USE_LUT 0x1
+
+typedef struct osm_v10_args {
+  int32_t abi_version;          /* = OSM_ABI_VERSION */
+  int32_t flags;                /* OSM_V10_USE_LUT */
+  int64_t B, S, H, hd, K;       /* 1 <= K <= 8 */
+  int64_t chunk;                /* tokens per Lion step, >= 1 */
+  const void* x;                /* [B,S,H*hd], x_dtype; lane stride 1 */
+  int32_t x_dtype;
+  int64_t x_stride_b, x_stride_s;
+  float* out;                   /* [B,S,H*hd] fp32 (values rounded to bf16) */
+  int64_t out_stride_b, out_stride_s;
+  const float* coeffs;          /* [B,H,K,hd] fp32, lane stride 1 */
+  int64_t c_stride_b, c_stride_h, c_stride_k;
+  const float* momentum;        /* [B,H,K,hd] fp32, lane stride 1 */
+  int64_t m_stride_b, m_stride_h, m_stride_k;
+  float* coeffs_out;            /* [B,H,K,hd] fp32 contiguous: after the last chunk */
+  float* momentum_out;          /* [B,H,K,hd] fp32 contiguous */
+  const float* lut;             /* [8,256] fp32: T_k on the table grid (with OSM_V10_USE_LUT) */
+  const float* lion_lambda;     /* [H] */
+  const float* lr_scale;        /* [H] */
+  const float* spectral_scale;  /* [K] */
+  const float* gate;            /* optional [B]: scales lr */
+  const float* dyn_lambda;      /* optional [B]: moves lam_h */
+  float ema_momentum, base_lr, beta1, beta2, weight_decay;
+  void* z_save;                 /* optional [B,S,H*hd] bf16: z of every token (for the backward) */
+  int64_t z_stride_b, z_stride_s;
+  float* coeff_hist;            /* optional [ceil(S/chunk),B,H,K,hd] fp32: the coefficients each chunk used */
+} osm_v10_args;
+
 /* Which entry point a workspace is sized for. */
 typedef enum osm_op { OSM_OP_FWD = 0, OSM_OP_TTT = 1, OSM_OP_BWD = 2 } osm_op;
 
@@ -168,6 +220,10 @@ int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t worksp
  * contiguous and is overwritten.  `target` is an osm_ttt_target. */
 int osm_cheby_ema_ttt(const osm_cheby_args* args, float* grad, int target, void* workspace,
                       size_t workspace_bytes, void* stream);
+
+/* The full-path chunk loop described above osm_v10_args, in one launch on
+ * `stream`.  Needs no workspace. */
+int osm_v10_chunked_ttt(const osm_v10_args* args, void* stream);
 
 /* Backward of osm_cheby_ema_fwd: writes grad_x and, when non-NULL,
  * grad_coeffs and grad_init.  Replaces the backward listed in the header

@@ -23,6 +23,7 @@ TARGET_SOFTSIGN = 1
 OP_FWD = 0
 OP_TTT = 1
 OP_BWD = 2
+V10_USE_LUT = 0x1
 
 STATUS = {
     0: "OSM_OK",
@@ -43,6 +44,7 @@ EXPORTS = (
     "osm_cheby_ema_fwd",
     "osm_cheby_ema_ttt",
     "osm_cheby_ema_bwd",
+    "osm_v10_chunked_ttt",
 )
 
 
@@ -99,6 +101,53 @@ class BwdArgs(ctypes.Structure):
     ]
 
 
+class V10Args(ctypes.Structure):
+    """Mirror of ``osm_v10_args``."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+        ("B", ctypes.c_int64),
+        ("S", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("hd", ctypes.c_int64),
+        ("K", ctypes.c_int64),
+        ("chunk", ctypes.c_int64),
+        ("x", ctypes.c_void_p),
+        ("x_dtype", ctypes.c_int32),
+        ("x_stride_b", ctypes.c_int64),
+        ("x_stride_s", ctypes.c_int64),
+        ("out", ctypes.c_void_p),
+        ("out_stride_b", ctypes.c_int64),
+        ("out_stride_s", ctypes.c_int64),
+        ("coeffs", ctypes.c_void_p),
+        ("c_stride_b", ctypes.c_int64),
+        ("c_stride_h", ctypes.c_int64),
+        ("c_stride_k", ctypes.c_int64),
+        ("momentum", ctypes.c_void_p),
+        ("m_stride_b", ctypes.c_int64),
+        ("m_stride_h", ctypes.c_int64),
+        ("m_stride_k", ctypes.c_int64),
+        ("coeffs_out", ctypes.c_void_p),
+        ("momentum_out", ctypes.c_void_p),
+        ("lut", ctypes.c_void_p),
+        ("lion_lambda", ctypes.c_void_p),
+        ("lr_scale", ctypes.c_void_p),
+        ("spectral_scale", ctypes.c_void_p),
+        ("gate", ctypes.c_void_p),
+        ("dyn_lambda", ctypes.c_void_p),
+        ("ema_momentum", ctypes.c_float),
+        ("base_lr", ctypes.c_float),
+        ("beta1", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("weight_decay", ctypes.c_float),
+        ("z_save", ctypes.c_void_p),
+        ("z_stride_b", ctypes.c_int64),
+        ("z_stride_s", ctypes.c_int64),
+        ("coeff_hist", ctypes.c_void_p),
+    ]
+
+
 class OsmError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"{STATUS.get(code, code)}: {msg}")
@@ -139,6 +188,8 @@ def load() -> ctypes.CDLL:
         lib.osm_cheby_ema_bwd.restype = ctypes.c_int
         lib.osm_cheby_ema_bwd.argtypes = [ctypes.POINTER(ChebyArgs), ctypes.POINTER(BwdArgs), ctypes.c_void_p,
                                           ctypes.c_size_t, ctypes.c_void_p]
+        lib.osm_v10_chunked_ttt.restype = ctypes.c_int
+        lib.osm_v10_chunked_ttt.argtypes = [ctypes.POINTER(V10Args), ctypes.c_void_p]
         got = lib.osm_abi_version()
         if got != ABI_VERSION:
             raise ImportError(f"orthossm_amd: library ABI {got} != binding ABI {ABI_VERSION}; rebuild")

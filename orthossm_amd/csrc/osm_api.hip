@@ -307,6 +307,88 @@ int osm_cheby_ema_ttt(const osm_cheby_args* args, float* grad, int target, void*
   return ok();
 }
 
+int osm_v10_chunked_ttt(const osm_v10_args* a, void* stream) {
+  if (!a) return fail(OSM_E_ARG, "args is NULL");
+  if (a->abi_version != OSM_ABI_VERSION)
+    return fail(OSM_E_ARG, "abi_version %d does not match library ABI %d", a->abi_version, OSM_ABI_VERSION);
+  if (a->flags & ~OSM_V10_USE_LUT) return fail(OSM_E_ARG, "unknown flag bits 0x%x", a->flags);
+  if (a->B < 0 || a->S < 0 || a->H < 1 || a->hd < 1)
+    return fail(OSM_E_SHAPE, "need B, S >= 0, H, hd >= 1 (B=%lld S=%lld H=%lld hd=%lld)", (long long)a->B,
+                (long long)a->S, (long long)a->H, (long long)a->hd);
+  if (a->K < 1 || a->K > OSM_MAX_K) return fail(OSM_E_SHAPE, "K=%lld outside [1, %d]", (long long)a->K, OSM_MAX_K);
+  if (a->chunk < 1) return fail(OSM_E_SHAPE, "chunk=%lld must be >= 1", (long long)a->chunk);
+  if (a->x_dtype != OSM_F32 && a->x_dtype != OSM_BF16) return fail(OSM_E_DTYPE, "x_dtype %d unsupported", a->x_dtype);
+  const int64_t D = a->H * a->hd;
+  if (D > (int64_t(1) << 28) || a->S >= (int64_t(1) << 31) || a->chunk >= (int64_t(1) << 31))
+    return fail(OSM_E_SHAPE, "problem too large");
+  if (a->S == 0) return fail(OSM_E_SHAPE, "the full path needs S >= 1");
+  if (a->B == 0) return ok();
+  if (!a->x || !a->out || !a->coeffs || !a->momentum || !a->coeffs_out || !a->momentum_out || !a->lion_lambda ||
+      !a->lr_scale || !a->spectral_scale || ((a->flags & OSM_V10_USE_LUT) && !a->lut))
+    return fail(OSM_E_ARG, "x, out, coeffs, momentum, coeffs_out, momentum_out, lion_lambda, lr_scale, "
+                           "spectral_scale (and lut with OSM_V10_USE_LUT) must be non-NULL");
+  const int xs = a->x_dtype == OSM_F32 ? 4 : 2;
+  if ((uintptr_t)a->x % xs || (uintptr_t)a->out % 4 || a->x_stride_b < 0 || a->x_stride_s < 0)
+    return fail(OSM_E_LAYOUT, "x and out must be element-aligned with non-negative strides");
+  if (a->out_stride_s < D || a->out_stride_b < a->S * a->out_stride_s)
+    return fail(OSM_E_LAYOUT, "out rows/batches overlap");
+  if (a->z_save && (a->z_stride_s < D || a->z_stride_b < a->S * a->z_stride_s || (uintptr_t)a->z_save % 2))
+    return fail(OSM_E_LAYOUT, "z_save rows/batches overlap or z_save misaligned");
+  // Each batch row is addressed through one buffer descriptor (31-bit byte offsets).
+  const int64_t lim = int64_t(1) << 31;
+  if (((a->S - 1) * a->x_stride_s + D) * xs >= lim || ((a->S - 1) * a->out_stride_s + D) * 4 >= lim ||
+      (a->z_save && ((a->S - 1) * a->z_stride_s + D) * 2 >= lim))
+    return fail(OSM_E_LAYOUT, "a batch row spans more than 2 GiB");
+  if (a->c_stride_b < 0 || a->c_stride_h < 0 || a->c_stride_k < 0 || a->m_stride_b < 0 || a->m_stride_h < 0 ||
+      a->m_stride_k < 0)
+    return fail(OSM_E_LAYOUT, "coeffs/momentum strides must be non-negative");
+  osm::V10Params p{};
+  p.x = a->x;
+  p.out = a->out;
+  p.coeffs = a->coeffs;
+  p.momentum = a->momentum;
+  p.coeffs_out = a->coeffs_out;
+  p.momentum_out = a->momentum_out;
+  p.lut = a->lut;
+  p.lion_lambda = a->lion_lambda;
+  p.lr_scale = a->lr_scale;
+  p.spectral_scale = a->spectral_scale;
+  p.gate = a->gate;
+  p.dyn_lambda = a->dyn_lambda;
+  p.z_save = a->z_save;
+  p.coeff_hist = a->coeff_hist;
+  p.x_sb = a->x_stride_b;
+  p.x_ss = a->x_stride_s;
+  p.o_sb = a->out_stride_b;
+  p.o_ss = a->out_stride_s;
+  p.z_sb = a->z_stride_b;
+  p.z_ss = a->z_stride_s;
+  p.c_sb = a->c_stride_b;
+  p.c_sh = a->c_stride_h;
+  p.c_sk = a->c_stride_k;
+  p.m_sb = a->m_stride_b;
+  p.m_sh = a->m_stride_h;
+  p.m_sk = a->m_stride_k;
+  p.B = (int)a->B;
+  p.S = (int)a->S;
+  p.H = (int)a->H;
+  p.hd = (int)a->hd;
+  p.K = (int)a->K;
+  p.D = (int)D;
+  p.chunk = (int)std::min<int64_t>(a->chunk, a->S);
+  p.n_lg = (int)((a->hd + osm::kV10Lanes - 1) / osm::kV10Lanes);
+  p.mu = a->ema_momentum;
+  p.base_lr = a->base_lr;
+  p.beta1 = a->beta1;
+  p.beta2 = a->beta2;
+  p.wd = a->weight_decay;
+  if ((int64_t)p.B * p.H * p.n_lg >= (int64_t(1) << 31)) return fail(OSM_E_SHAPE, "problem too large");
+  const hipError_t e = osm::launch_v10(p, a->x_dtype, (a->flags & OSM_V10_USE_LUT) != 0, a->K <= 4 ? 4 : 8,
+                                       static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "full-path kernel launch");
+  return ok();
+}
+
 int osm_cheby_ema_bwd(const osm_cheby_args* args, const osm_cheby_bwd_args* bwd, void* workspace,
                       size_t workspace_bytes, void* stream) {
   Geometry geo;

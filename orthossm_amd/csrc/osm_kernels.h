@@ -119,6 +119,33 @@ struct BwdParams {
   float* grad_coeffs;          // [B,H,K,hd]
 };
 
+// Full-path launch (online TTT over chunks with an inline Lion update): one
+// workgroup per (batch row, head, group of kV10Lanes lanes) walks the chunks in
+// order.  Needs no workspace.
+constexpr int kV10Lanes = 16;     // lanes per workgroup
+constexpr int kV10Groups = 32;    // token groups (runs) per 256-token block
+constexpr int kV10Run = 8;        // tokens per run
+struct V10Params {
+  const void* x;
+  float* out;
+  const float* coeffs;
+  const float* momentum;
+  float* coeffs_out;
+  float* momentum_out;
+  const float* lut;            // [8][256] fp32 (LUT mode)
+  const float* lion_lambda;    // [H]
+  const float* lr_scale;       // [H]
+  const float* spectral_scale; // [K]
+  const float* gate;           // [B] or NULL
+  const float* dyn_lambda;     // [B] or NULL
+  void* z_save;                // bf16 [B,S,D] or NULL
+  float* coeff_hist;           // [n_chunks][B,H,K,hd] or NULL
+  int64_t x_sb, x_ss, o_sb, o_ss, z_sb, z_ss;
+  int64_t c_sb, c_sh, c_sk, m_sb, m_sh, m_sk;
+  int B, S, H, hd, K, D, chunk, n_lg;
+  float mu, base_lr, beta1, beta2, wd;
+};
+
 // Workspace layout helpers (bytes).
 size_t slot_words(bool dyn);
 size_t fwd_workspace_bytes(int n_lb, int n_tiles, int lanes, bool dyn);
@@ -133,6 +160,7 @@ hipError_t launch_ttt(const FwdParams& p, float* grad, int x_dtype, int out_dtyp
                       int kpad, hipStream_t stream);
 hipError_t launch_bwd(const BwdParams& p, int x_dtype, int out_dtype, bool dyn, int tile, int kpad,
                       hipStream_t stream);
+hipError_t launch_v10(const V10Params& p, int x_dtype, bool use_lut, int kpad, hipStream_t stream);
 hipError_t launch_fill_zero(void* ptr, size_t bytes, hipStream_t stream);
 hipError_t launch_copy_state(const float* src, float* dst, size_t n, hipStream_t stream);
 

@@ -1,0 +1,273 @@
+// The reference's full apply_cheby_rkv_v10 path for gfx950: online TTT over
+// chunks with an inline Lion update, in one launch.
+//
+// Reference counterpart: the chunk loop of apply_cheby_rkv_v10
+// (sdpc_kernel.py:2574-2606), each chunk a FusedChebyRKVv10.forward
+// (2353-2433) running _ortho_megakernel (1890-2287): one kernel launch and a
+// few host-side casts per chunk, with the updated coefficients and momentum
+// fed to the next chunk.  Per chunk (length L <= chunk):
+//   x -> bf16; u = sign(x)(1 - 1/(1 + max(|x|, 1e-7))), NaN read as 0 and
+//   sign(0) = +1; y = LUT interpolation of sum_k c_k T_k(u) (256-point half
+//   table, odd terms times sign(u)) or the 4-term Clenshaw fallback;
+//   z = tanh(clamp(gamma_h y, -4, 4)) (0 for NaN x); s = mu s + (1-mu) z from 0;
+//   out = bf16(s); gc_k = sum over (t, t+1) of gv T_k(u_t) with
+//   gv = err / (1 + exp(-3|err|)), err = u_{t+1} - s_t; then Lion on (c, m).
+//
+// Chunks depend on each other only through (c, m) of each lane, so one
+// workgroup owns kV10Lanes lanes of one (batch row, head) and walks the
+// chunks in order; the dependency never leaves the workgroup.  A chunk is
+// processed in 256-token blocks: thread (group g, lane l) owns a run of
+// kV10Run tokens; runs are composed by a scan in LDS; the proxy-gradient
+// sums are reduced over the runs in a fixed order, and kV10Lanes * K threads
+// apply Lion and publish the next chunk's coefficients through LDS.
+#include "osm_tile.h"
+
+namespace osm {
+namespace {
+
+constexpr int kBlockTok = kV10Groups * kV10Run;      // 256 tokens per block
+constexpr int kV10Threads = kV10Groups * kV10Lanes;  // 512
+constexpr float kLog2e = 1.4426950408889634f;
+
+// x rounded to bf16 (round to nearest even), as the reference casts on entry.
+template <typename XT>
+__device__ __forceinline__ float to_bf16_value(float v);
+template <>
+__device__ __forceinline__ float to_bf16_value<float>(float v) {
+  return (float)(__bf16)v;
+}
+template <>
+__device__ __forceinline__ float to_bf16_value<__bf16>(float v) {
+  return v;   // loaded from bf16 already
+}
+
+// The megakernel's softsign on a bf16 value: |u| and sign(u); NaN reads as 0.
+__device__ __forceinline__ void v10_softsign(float xb, float& absu, float& sgn) {
+  const float xs = xb == xb ? xb : 0.0f;
+  const float ax = __builtin_fmaxf(__builtin_fabsf(xs), 1e-7f);
+  absu = 1.0f - 1.0f / (1.0f + ax);
+  sgn = xs >= 0.0f ? 1.0f : -1.0f;
+}
+
+struct V10Lds {
+  float lut[256][8];                 // T_k at the table's grid, k contiguous
+  float cs[8][kV10Lanes];            // coefficients of the current chunk
+  float ms[8][kV10Lanes];            // Lion momentum
+  float aggA[kV10Groups][kV10Lanes];
+  float aggB[kV10Groups][kV10Lanes];
+  float u0[kV10Groups][kV10Lanes];   // u at each run's first token
+  float carry[kV10Lanes];            // EMA state entering the block
+  float gc[kV10Groups][8][kV10Lanes];
+};
+
+template <typename XT, int KP, bool LUT>
+__global__ void __launch_bounds__(kV10Threads) v10_chunked_kernel(const V10Params p) {
+  __shared__ V10Lds L;
+  const int tid = threadIdx.x;
+  const int l = tid % kV10Lanes, g = tid / kV10Lanes;
+  const int lg = blockIdx.x % p.n_lg;
+  const int bh = blockIdx.x / p.n_lg;
+  const int h = bh % p.H, b = bh / p.H;
+  const int j = lg * kV10Lanes + l;                 // lane inside the head
+  const bool lane_ok = j < p.hd;
+  const int d = h * p.hd + j;
+
+  // Tables and the lanes' starting coefficients and momentum.
+  if constexpr (LUT) {
+    for (int i = tid; i < 256 * 8; i += kV10Threads) L.lut[i % 256][i / 256] = p.lut[i];
+  }
+  if (tid < KP * kV10Lanes) {
+    const int k = tid / kV10Lanes, ll = tid % kV10Lanes, jj = lg * kV10Lanes + ll;
+    const bool ok = jj < p.hd && k < p.K;
+    L.cs[k][ll] = ok ? p.coeffs[(int64_t)b * p.c_sb + (int64_t)h * p.c_sh + (int64_t)k * p.c_sk + jj] : 0.0f;
+    L.ms[k][ll] = ok ? p.momentum[(int64_t)b * p.m_sb + (int64_t)h * p.m_sh + (int64_t)k * p.m_sk + jj] : 0.0f;
+  }
+  const float gamma = 0.98f - 0.06f * (float)h / (float)p.H;
+  const float mu = p.mu, one_m = 1.0f - p.mu;
+
+  // Row descriptors over the whole sequence of this batch row.
+  const Rsrc xr = make_rsrc(static_cast<const char*>(p.x) + (int64_t)b * p.x_sb * sizeof(XT),
+                            ((uint64_t)(p.S - 1) * p.x_ss + p.D) * sizeof(XT));
+  const Rsrc orr = make_rsrc(reinterpret_cast<const char*>(p.out) + (int64_t)b * p.o_sb * 4,
+                             ((uint64_t)(p.S - 1) * p.o_ss + p.D) * 4);
+  Rsrc zr = orr;
+  if (p.z_save)
+    zr = make_rsrc(static_cast<const char*>(p.z_save) + (int64_t)b * p.z_sb * 2,
+                   ((uint64_t)(p.S - 1) * p.z_ss + p.D) * 2);
+  const uint32_t vx = lane_ok ? (uint32_t)(d * sizeof(XT)) : kOffOOB;
+  const uint32_t vo = lane_ok ? (uint32_t)(d * 4) : kOffOOB;
+  const uint32_t vz = lane_ok ? (uint32_t)(d * 2) : kOffOOB;
+  __syncthreads();
+
+  const int n_chunks = (p.S + p.chunk - 1) / p.chunk;
+  for (int ch = 0; ch < n_chunks; ++ch) {
+    const int t_chunk = ch * p.chunk;
+    const int len = min(p.chunk, p.S - t_chunk);
+    float c[KP];
+#pragma unroll
+    for (int k = 0; k < KP; ++k) c[k] = L.cs[k][l];
+    if (p.coeff_hist && g == 0 && lane_ok) {
+      float* hst = p.coeff_hist + (size_t)ch * p.B * p.H * p.K * p.hd + (((size_t)b * p.H + h) * p.K) * p.hd + j;
+      for (int k = 0; k < p.K && k < KP; ++k) hst[(size_t)k * p.hd] = c[k];
+    }
+    float gc[KP];
+#pragma unroll
+    for (int k = 0; k < KP; ++k) gc[k] = 0.0f;
+    if (tid < kV10Lanes) L.carry[tid] = 0.0f;
+
+    for (int blk = 0; blk * kBlockTok < len; ++blk) {
+      const int r0 = blk * kBlockTok + g * kV10Run;      // run start inside the chunk
+      const int n_valid = max(0, min(kV10Run, len - r0));
+      const int t0 = t_chunk + r0;                        // run start in the sequence
+      float u[kV10Run], w[kV10Run];
+      float A = 1.0f, Bv = 0.0f;
+#pragma unroll
+      for (int r = 0; r < kV10Run; ++r) {
+        float xv[1] = {0.0f};
+        if (r < n_valid) BufVec<XT, 1>::load(xr, vx, (uint32_t)((int64_t)(t0 + r) * p.x_ss * sizeof(XT)), xv);
+        const float xb = to_bf16_value<XT>(xv[0]);
+        float absu, sgn;
+        v10_softsign(xb, absu, sgn);
+        u[r] = sgn * absu;
+        float y;
+        if constexpr (LUT) {
+          const float fidx = absu * 255.0f;
+          const int i0 = min((int)fidx, 254);
+          const float fr = __builtin_fminf(__builtin_fmaxf(fidx - (float)i0, 0.0f), 1.0f);
+          float ye = 0.0f, yo = 0.0f;
+#pragma unroll
+          for (int k = 0; k < KP; ++k) {
+            const float ta = L.lut[i0][k], tb = L.lut[i0 + 1][k];
+            const float it = __builtin_fmaf(fr, tb - ta, ta);
+            if (k & 1)
+              yo = __builtin_fmaf(c[k], it, yo);
+            else
+              ye = __builtin_fmaf(c[k], it, ye);
+          }
+          y = __builtin_fmaf(sgn, yo, ye);
+        } else {
+          const float uu = u[r], u2 = uu + uu;
+          const float c3 = KP > 3 ? c[3] : 0.0f, c2 = KP > 2 ? c[2] : 0.0f;
+          const float b2 = __builtin_fmaf(u2, c3, c2);
+          const float b1 = __builtin_fmaf(u2, b2, c[1]) - c3;
+          y = __builtin_fmaf(uu, b1, c[0]) - b2;
+        }
+        const float yc = __builtin_amdgcn_fmed3f(gamma * y, -4.0f, 4.0f);
+        const float e2 = __builtin_amdgcn_exp2f(2.0f * kLog2e * yc);
+        float z = (e2 - 1.0f) / (e2 + 1.0f);
+        z = xb == xb ? z : 0.0f;
+        w[r] = one_m * z;
+        if (r < n_valid) {
+          Bv = __builtin_fmaf(mu, Bv, w[r]);
+          A *= mu;
+        }
+        if (p.z_save && r < n_valid) {
+          const float zz[1] = {z};
+          BufVec<__bf16, 1>::store(zr, vz, (uint32_t)((int64_t)(t0 + r) * p.z_ss * 2), zz);
+        }
+      }
+      // u after the run: the next run's first token, or for the block's last
+      // run the first token after the block (inside the chunk).
+      float u_after = 0.0f;
+      if (g == kV10Groups - 1 && r0 + kV10Run < len) {
+        float xv[1];
+        BufVec<XT, 1>::load(xr, vx, (uint32_t)((int64_t)(t0 + kV10Run) * p.x_ss * sizeof(XT)), xv);
+        float absu, sgn;
+        v10_softsign(to_bf16_value<XT>(xv[0]), absu, sgn);
+        u_after = sgn * absu;
+      }
+      L.aggA[g][l] = A;
+      L.aggB[g][l] = Bv;
+      L.u0[g][l] = u[0];
+      __syncthreads();
+      float s = L.carry[l];
+      for (int q = 0; q < g; ++q) s = __builtin_fmaf(L.aggA[q][l], s, L.aggB[q][l]);
+      if (g < kV10Groups - 1) u_after = L.u0[g + 1][l];
+      // Replay, store bf16(s), proxy gradient.
+#pragma unroll
+      for (int r = 0; r < kV10Run; ++r) {
+        if (r < n_valid) {
+          s = __builtin_fmaf(mu, s, w[r]);
+          const float so = __builtin_amdgcn_fmed3f(s, -1.0f, 1.0f);
+          const float ov[1] = {(float)(__bf16)so};
+          BufVec<float, 1>::store(orr, vo, (uint32_t)((int64_t)(t0 + r) * p.o_ss * 4), ov);
+          if (r0 + r + 1 < len) {
+            const float un = r + 1 < kV10Run ? u[r + 1] : u_after;
+            const float err = un - so;
+            const float gv = err / (1.0f + __builtin_amdgcn_exp2f(-3.0f * kLog2e * __builtin_fabsf(err)));
+            const float uu = u[r], u2 = uu + uu;
+            gc[0] += gv;
+            if constexpr (KP > 1) gc[1] = __builtin_fmaf(gv, uu, gc[1]);
+            float tm2 = 1.0f, tm1 = uu;
+#pragma unroll
+            for (int k = 2; k < KP; ++k) {
+              const float tk = __builtin_fmaf(u2, tm1, -tm2);
+              gc[k] = __builtin_fmaf(gv, tk, gc[k]);
+              tm2 = tm1;
+              tm1 = tk;
+            }
+          }
+        }
+      }
+      __syncthreads();   // all reads of carry / aggregates / u0 done
+      if (g == kV10Groups - 1) {
+        // state after the block's last valid token (invalid tokens are skipped)
+        L.carry[l] = s;
+      }
+      __syncthreads();
+    }
+
+    // Reduce the proxy gradient over the runs (fixed order), then Lion.
+#pragma unroll
+    for (int k = 0; k < KP; ++k) L.gc[g][k][l] = gc[k];
+    __syncthreads();
+    if (tid < KP * kV10Lanes) {
+      const int k = tid / kV10Lanes, ll = tid % kV10Lanes;
+      float G = 0.0f;
+      for (int q = 0; q < kV10Groups; ++q) G += L.gc[q][k][ll];
+      if (k < p.K) {
+        const float inv_s = 1.0f / (float)(len - 1);   // len = 1: inf, as the reference (NaN momentum)
+        const float gk = G * inv_s;
+        float lr = p.base_lr * p.lr_scale[h];
+        float lam = p.lion_lambda[h];
+        if (p.dyn_lambda) lam = __builtin_fminf(__builtin_fmaxf(lam + 0.008f * (p.dyn_lambda[b] - 0.5f), 0.90f), 0.9999f);
+        if (p.gate) lr *= p.gate[b];
+        const float decay = lam - lr * p.wd;
+        const float m = L.ms[k][ll];
+        const float interp = p.beta1 * m + (1.0f - p.beta1) * gk;
+        const float sg = interp > 0.0f ? 1.0f : (interp < 0.0f ? -1.0f : 0.0f);
+        L.ms[k][ll] = p.beta2 * m + (1.0f - p.beta2) * gk;
+        L.cs[k][ll] = decay * L.cs[k][ll] + lr * p.spectral_scale[k] * sg;
+      }
+    }
+    __syncthreads();
+  }
+
+  if (tid < KP * kV10Lanes) {
+    const int k = tid / kV10Lanes, ll = tid % kV10Lanes, jj = lg * kV10Lanes + ll;
+    if (jj < p.hd && k < p.K) {
+      const size_t o = (((size_t)b * p.H + h) * p.K + k) * p.hd + jj;
+      p.coeffs_out[o] = L.cs[k][ll];
+      p.momentum_out[o] = L.ms[k][ll];
+    }
+  }
+}
+
+template <typename XT, bool LUT>
+hipError_t launch_x(const V10Params& p, int kpad, hipStream_t stream) {
+  const unsigned grid = (unsigned)(p.B * p.H * p.n_lg);
+  if (kpad == 4)
+    hipLaunchKernelGGL((v10_chunked_kernel<XT, 4, LUT>), dim3(grid), dim3(kV10Threads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((v10_chunked_kernel<XT, 8, LUT>), dim3(grid), dim3(kV10Threads), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_v10(const V10Params& p, int x_dtype, bool use_lut, int kpad, hipStream_t stream) {
+  if (x_dtype == 0) return use_lut ? launch_x<float, true>(p, kpad, stream) : launch_x<float, false>(p, kpad, stream);
+  return use_lut ? launch_x<__bf16, true>(p, kpad, stream) : launch_x<__bf16, false>(p, kpad, stream);
+}
+
+}  // namespace osm

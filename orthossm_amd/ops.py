@@ -5,6 +5,8 @@
 ``cheby_ema_backward``  dL/dx, dL/dc, dL/d ema_init from dL/dout (+ dL/d ema_final).
 ``cheby_ema``           the forward as a differentiable op (autograd.Function
                         whose backward is ``cheby_ema_backward``).
+``v10_chunked_ttt``     the reference's full path: online TTT over chunks with
+                        an inline Lion update, in one launch.
 
 All run on the current torch stream of the input's device and never
 synchronise the host.  Inputs are not modified.  There is no CPU path: a
@@ -298,6 +300,123 @@ def cheby_ema(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, *, g: torch.T
     out, fin = _ChebyEMAFunction.apply(x, coeffs, ema_init, damping, lam, g, lam_shift, lam_min, lam_max, clamp,
                                        out_dtype, nan_policy)
     return (out, fin) if return_state else out
+
+
+# Per-head Lion forget factors of the reference (MULTI_SCALE_LAMBDA,
+# sdpc_kernel.py:1416); heads past the eighth use 0.995 (1429-1432).
+V10_LION_LAMBDA = (0.9995, 0.9995, 0.997, 0.997, 0.995, 0.995, 0.97, 0.95)
+_v10_lock = threading.Lock()
+_v10_cache: dict = {}
+
+
+def v10_tables(device: torch.device, n_heads: int, K: int):
+    """(lut [8,256], lion_lambda [H], spectral_scale [K], lr_scale [H]) fp32 on
+    ``device``: the Chebyshev table T_k(linspace(0, 1, 256)) built in fp32 by
+    the recurrence (sdpc_kernel.py:63-81) and the Lion constants
+    (sdpc_kernel.py:1423-1437).  Cached per (device, H, K)."""
+    key = (device.type, device.index, n_heads, K)
+    with _v10_lock:
+        hit = _v10_cache.get(key)
+        if hit is not None:
+            return hit
+        grid = torch.linspace(0.0, 1.0, 256)
+        T = torch.zeros(8, 256)
+        T[0] = 1.0
+        T[1] = grid
+        for k in range(2, 8):
+            T[k] = 2.0 * grid * T[k - 1] - T[k - 2]
+        n_active = min(n_heads, len(V10_LION_LAMBDA))
+        lam = torch.tensor(list(V10_LION_LAMBDA[:n_active]) + [0.995] * max(0, n_heads - n_active))
+        ss = 1.0 / (torch.arange(K, dtype=torch.float32) + 1.0) ** 1.5
+        h = torch.arange(n_heads, dtype=torch.float32)
+        lr_scale = 1.0 + 0.25 * (h - n_heads / 2.0) / max(n_heads, 1)
+        hit = tuple(t.to(device=device, dtype=torch.float32).contiguous() for t in (T, lam, ss, lr_scale))
+        _v10_cache[key] = hit
+        return hit
+
+
+def v10_chunked_ttt(x: torch.Tensor, coeffs: torch.Tensor, momentum: torch.Tensor, *, n_heads: int,
+                    base_lr: float = 0.005, ema_momentum: float = 0.9, beta1: float = 0.9, beta2: float = 0.99,
+                    weight_decay: float = 0.01, chunk_size: int = 256, gate_global: torch.Tensor | None = None,
+                    dynamic_lambda: torch.Tensor | None = None, use_lut: bool = True,
+                    save_for_backward: bool = False):
+    """The reference's full apply_cheby_rkv_v10 path in one launch: chunks of
+    ``chunk_size`` tokens, each with the coefficients and Lion momentum the
+    previous chunk left (see osm_v10_args in include/osm.h).
+
+    x [B,S,D] fp32|bf16, coeffs and momentum [B,H,K,hd] (cast to fp32; K > 8:
+    coefficients past the eighth are returned unchanged, as the reference's
+    kernel leaves them), gate_global / dynamic_lambda optional [B].  Returns
+    (out [B,S,D] fp32 holding bf16 values, coeffs_new, momentum_new) and, with
+    save_for_backward, also (z [B,S,D] bf16, coeff_hist [n_chunks,B,H,K,hd]).
+    """
+    lib = nat.load()
+    if not isinstance(x, torch.Tensor) or x.dim() != 3:
+        raise ValueError("x must be a [B,S,D] tensor")
+    if x.device.type != "cuda":
+        raise RuntimeError("orthossm_amd runs on a ROCm GPU only; x is on " + str(x.device))
+    if momentum is None:
+        raise ValueError("the full path needs a momentum buffer [B,H,K,hd]")
+    dev = x.device
+    B, S, D = x.shape
+    if S == 0:
+        raise ValueError("the full path needs S >= 1")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        x = x.float()
+    if x.stride(2) != 1:
+        x = x.contiguous()
+    c_full = coeffs.to(device=dev, dtype=torch.float32)
+    m_full = momentum.to(device=dev, dtype=torch.float32)
+    if c_full.dim() != 4 or c_full.shape[0] != B or c_full.shape[1] != n_heads or \
+            c_full.shape[1] * c_full.shape[3] != D or m_full.shape != c_full.shape:
+        raise ValueError(f"coeffs/momentum must be [B,H,K,hd] matching x {tuple(x.shape)} and n_heads={n_heads}")
+    H, Kfull, hd = n_heads, c_full.shape[2], c_full.shape[3]
+    K = min(Kfull, nat.MAX_K)
+    c = c_full[:, :, :K]
+    m = m_full[:, :, :K]
+    if c.stride(3) != 1:
+        c = c.contiguous()
+    if m.stride(3) != 1:
+        m = m.contiguous()
+    lut, lion_lambda, ss, lr_scale = v10_tables(dev, H, K)
+    out = torch.empty((B, S, D), device=dev, dtype=torch.float32)
+    c_out = torch.empty((B, H, K, hd), device=dev, dtype=torch.float32)
+    m_out = torch.empty_like(c_out)
+    gate = None if gate_global is None else gate_global.to(device=dev, dtype=torch.float32).reshape(B).contiguous()
+    dyn = None if dynamic_lambda is None else \
+        dynamic_lambda.to(device=dev, dtype=torch.float32).reshape(B).contiguous()
+    n_chunks = (S + chunk_size - 1) // chunk_size
+    z = hist = None
+    if save_for_backward:
+        z = torch.empty((B, S, D), device=dev, dtype=torch.bfloat16)
+        hist = torch.empty((n_chunks, B, H, K, hd), device=dev, dtype=torch.float32)
+    a = nat.V10Args()
+    a.abi_version = nat.ABI_VERSION
+    a.flags = nat.V10_USE_LUT if use_lut else 0
+    a.B, a.S, a.H, a.hd, a.K, a.chunk = B, S, H, hd, K, int(chunk_size)
+    a.x, a.x_dtype, a.x_stride_b, a.x_stride_s = x.data_ptr(), _dtype_code(x.dtype), x.stride(0), x.stride(1)
+    a.out, a.out_stride_b, a.out_stride_s = out.data_ptr(), out.stride(0), out.stride(1)
+    a.coeffs, a.c_stride_b, a.c_stride_h, a.c_stride_k = c.data_ptr(), c.stride(0), c.stride(1), c.stride(2)
+    a.momentum, a.m_stride_b, a.m_stride_h, a.m_stride_k = m.data_ptr(), m.stride(0), m.stride(1), m.stride(2)
+    a.coeffs_out, a.momentum_out = c_out.data_ptr(), m_out.data_ptr()
+    a.lut, a.lion_lambda, a.lr_scale, a.spectral_scale = lut.data_ptr(), lion_lambda.data_ptr(), \
+        lr_scale.data_ptr(), ss.data_ptr()
+    a.gate = gate.data_ptr() if gate is not None else None
+    a.dyn_lambda = dyn.data_ptr() if dyn is not None else None
+    a.ema_momentum, a.base_lr, a.beta1, a.beta2, a.weight_decay = (float(ema_momentum), float(base_lr),
+                                                                   float(beta1), float(beta2), float(weight_decay))
+    if z is not None:
+        a.z_save, a.z_stride_b, a.z_stride_s = z.data_ptr(), z.stride(0), z.stride(1)
+        a.coeff_hist = hist.data_ptr()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    nat.check(lib.osm_v10_chunked_ttt(ctypes.byref(a), ctypes.c_void_p(stream)))
+    keep = (x, c, m, gate, dyn)  # noqa: F841  (alive until the launch is queued)
+    if Kfull > K:
+        c_out = torch.cat([c_out, c_full[:, :, K:]], dim=2)
+        m_out = torch.cat([m_out, m_full[:, :, K:]], dim=2)
+    if save_for_backward:
+        return out, c_out, m_out, z, hist
+    return out, c_out, m_out
 
 
 def _check_dest(t: torch.Tensor, shape, dev, name: str) -> None:

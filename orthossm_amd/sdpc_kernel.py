@@ -16,15 +16,18 @@ reference's autograd does through that path (its EMA backward
 _EMAFastPathFn.backward, sdpc_kernel.py:1677-1701, masks the adjoint with
 |out| < 1 - 1e-6).
 
-Not covered yet: the full path with online Lion TTT over 256-token chunks
-(``FusedChebyRKVv10``, sdpc_kernel.py:2351-2515).  It raises
-``NotImplementedError`` instead of silently changing semantics.
+The full path (``S >= seq_threshold``; sdpc_kernel.py:2559-2606: online TTT
+over ``chunk_size``-token chunks, each a ``FusedChebyRKVv10.forward`` with the
+inline Lion update, LUT or 4-term Clenshaw series, clamped tanh, EMA restarted
+at every chunk, bf16 rounding of x and of the output) runs as one launch of
+``v10_chunked_ttt``.  Gradients through the full path are not covered yet and
+raise ``NotImplementedError``.
 """
 from __future__ import annotations
 
 import torch
 
-from .ops import cheby_ema, cheby_ema_forward
+from .ops import cheby_ema, cheby_ema_forward, v10_chunked_ttt
 
 
 def v10_damping(n_heads: int, device=None) -> torch.Tensor:
@@ -44,14 +47,17 @@ def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_m
         coeffs = coeffs.float()
     if momentum_buf is not None and momentum_buf.dtype != torch.float32:
         momentum_buf = momentum_buf.float()
-    if not (seq_threshold > 0 and S < seq_threshold):
-        raise NotImplementedError(
-            "orthossm_amd: the full path (online Lion TTT over chunks, S >= seq_threshold) is not "
-            "implemented; call with seq_threshold > S for the fixed-coefficient path, or use "
-            "orthossm_amd.cheby_ema_ttt for the fused TTT gradient.")
     H = n_heads
     if D % H:
         raise ValueError(f"D={D} is not divisible by n_heads={H}")
+    if not (seq_threshold > 0 and S < seq_threshold):
+        if torch.is_grad_enabled() and (x.requires_grad or coeffs.requires_grad):
+            raise NotImplementedError("orthossm_amd: gradients through the full path are not implemented yet")
+        out, c_new, m_new = v10_chunked_ttt(
+            x, coeffs, momentum_buf, n_heads=H, base_lr=base_lr, ema_momentum=ema_momentum, beta1=lion_beta1,
+            beta2=lion_beta2, weight_decay=lion_wd, chunk_size=chunk_size, gate_global=gate_global,
+            dynamic_lambda=dynamic_lambda, use_lut=use_lut)
+        return out, c_new, m_new
     damping = v10_damping(H, x.device)
     lam = torch.full((H,), float(ema_momentum), dtype=torch.float32, device=x.device)
     if torch.is_grad_enabled() and (x.requires_grad or coeffs.requires_grad):

@@ -35,7 +35,8 @@ def test_every_declared_function_is_exported():
         assert hasattr(lib, name), name
 
 
-@pytest.mark.parametrize("cls,cname", [(nat.ChebyArgs, "osm_cheby_args"), (nat.BwdArgs, "osm_cheby_bwd_args")])
+@pytest.mark.parametrize("cls,cname", [(nat.ChebyArgs, "osm_cheby_args"), (nat.BwdArgs, "osm_cheby_bwd_args"),
+                                      (nat.V10Args, "osm_v10_args")])
 def test_struct_layout_matches_ctypes(cls, cname):
     fields = [f for f, _ in cls._fields_]
     prog = ['#include <stdio.h>', '#include <stddef.h>', '#include "osm.h"', "int main(void){",
@@ -158,6 +159,38 @@ def test_bwd_argument_errors(akw, bkw, code):
     assert lib.osm_cheby_ema_bwd(ctypes.byref(a), ctypes.byref(b), None, 0, None) == code
     assert lib.osm_last_error() != b""
     assert lib.osm_cheby_ema_bwd(ctypes.byref(_args()), None, None, 0, None) == -1
+
+
+def _v10(**kw):
+    a = nat.V10Args()
+    a.abi_version = nat.ABI_VERSION
+    a.flags = nat.V10_USE_LUT
+    a.B, a.S, a.H, a.hd, a.K, a.chunk = 2, 1000, 4, 16, 8, 256
+    a.x = a.out = a.coeffs = a.momentum = a.coeffs_out = a.momentum_out = 0x10000
+    a.lut = a.lion_lambda = a.lr_scale = a.spectral_scale = 0x10000
+    a.x_stride_b = a.out_stride_b = 1000 * 64
+    a.x_stride_s = a.out_stride_s = 64
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(abi_version=3), -1),
+    (dict(flags=0x10), -1),
+    (dict(K=9), -2),
+    (dict(chunk=0), -2),
+    (dict(S=0), -2),
+    (dict(x_dtype=5), -3),
+    (dict(lut=0), -1),                 # LUT mode needs the table
+    (dict(momentum=0), -1),
+    (dict(out_stride_s=32), -4),       # rows overlap
+    (dict(x_stride_s=1 << 22), -4),    # a batch row over 2 GiB
+])
+def test_v10_argument_errors(kw, code):
+    lib = nat.load()
+    assert lib.osm_v10_chunked_ttt(ctypes.byref(_v10(**kw)), None) == code
+    assert lib.osm_last_error() != b""
 
 
 def test_error_messages_are_thread_local():

@@ -1,0 +1,134 @@
+"""GPU parity of the full apply_cheby_rkv_v10 path (osm_v10_chunked_ttt
+through the C ABI) against the CPU restatement in oracle/v10_full.py."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import v10_full as V
+from orthossm_amd import apply_cheby_rkv_v10
+from orthossm_amd.ops import v10_chunked_ttt
+
+pytestmark = pytest.mark.gpu
+
+
+def case(B, S, H, hd, K, seed, mom_scale=0.0):
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, S, H * hd, generator=gen)
+    c = torch.randn(B, H, K, hd, generator=gen) / torch.arange(1, K + 1).view(1, 1, K, 1)
+    m = torch.randn(B, H, K, hd, generator=gen) * mom_scale
+    return x, c, m
+
+
+def compare(out, cn, mn, want):
+    wo, wc, wm = want
+    o = out.cpu().numpy().astype(np.float64)
+    # out holds bf16 values: equal except where fp32/fp64 rounding of s lands
+    # on the other side of a bf16 rounding boundary (one bf16 ulp).
+    diff = np.abs(o - wo)
+    assert np.nanmax(np.where(np.isnan(wo), 0, diff)) <= 2e-2, "out beyond 2e-2"
+    assert (diff > 1e-6).mean() <= 1e-3, f"{(diff > 1e-6).mean():.4f} of out differ"
+    # coefficients/momentum: fp32 against float64; a Lion sign decided by
+    # rounding (|interp| ~ 1e-7) moves one coefficient by 2 lr ss_k, so allow
+    # a tiny fraction of such elements.
+    for got, w, what in ((cn, wc, "coeffs"), (mn, wm, "momentum")):
+        g = got.cpu().numpy().astype(np.float64)
+        both = np.isnan(g) & np.isnan(w)
+        d = np.abs(np.where(both, 0, g) - np.where(both, 0, w))
+        assert not np.isnan(d).any(), f"{what}: NaN mismatch"
+        assert (d > 1e-5 * (1 + np.abs(w))).mean() <= 1e-3, f"{what}: {(d > 1e-5).sum()} elements off"
+
+
+def oracle(x, c, m, **kw):
+    return V.v10_full(x.numpy(), c.double().numpy(), m.double().numpy(), **kw)
+
+
+@pytest.mark.parametrize("B,S,H,hd,K,chunk,use_lut", [
+    (2, 600, 4, 16, 8, 256, True),      # 3 chunks, last partial
+    (2, 600, 4, 16, 8, 256, False),     # 4-term Clenshaw fallback
+    (1, 256, 2, 32, 4, 256, True),      # exactly one chunk, K <= 4 kernel
+    (3, 450, 2, 20, 8, 100, True),      # hd not a multiple of 16; chunk < 256
+    (2, 1300, 4, 16, 6, 512, True),     # chunks of two 256-token blocks
+    (1, 700, 8, 16, 8, 700, True),      # S <= chunk: one chunk of 700
+    (2, 257, 4, 16, 8, 256, True),      # a 1-token last chunk (NaN momentum, as the reference)
+])
+def test_v10_full_path_matches_oracle(dev, B, S, H, hd, K, chunk, use_lut):
+    x, c, m = case(B, S, H, hd, K, seed=S + K, mom_scale=0.01)
+    out, cn, mn = v10_chunked_ttt(x.to(dev), c.to(dev), m.to(dev), n_heads=H, chunk_size=chunk, use_lut=use_lut)
+    torch.cuda.synchronize()
+    compare(out, cn, mn, oracle(x, c, m, n_heads=H, chunk_size=chunk, use_lut=use_lut))
+
+
+def test_v10_gate_dynamic_lambda_and_hyperparameters(dev):
+    B, S, H, hd, K = 3, 700, 4, 16, 8
+    x, c, m = case(B, S, H, hd, K, seed=5)
+    gate = torch.tensor([0.3, 1.0, 2.5])
+    dyn = torch.tensor([0.1, 0.5, 0.95])
+    kw = dict(n_heads=H, base_lr=0.02, ema_momentum=0.8, beta1=0.85, beta2=0.95, chunk_size=256)
+    out, cn, mn = v10_chunked_ttt(x.to(dev), c.to(dev), m.to(dev), gate_global=gate.to(dev),
+                                  dynamic_lambda=dyn.to(dev), weight_decay=0.05, **kw)
+    torch.cuda.synchronize()
+    compare(out, cn, mn, oracle(x, c, m, gate_global=gate.numpy(), dynamic_lambda=dyn.numpy(), wd=0.05,
+                                **{k: v for k, v in kw.items()}))
+
+
+def test_v10_special_values_and_bf16_input(dev):
+    B, S, H, hd, K = 2, 520, 2, 16, 8
+    x, c, m = case(B, S, H, hd, K, seed=9)
+    x[0, 10, 3] = float("nan")
+    x[0, 11, 4] = 0.0
+    x[1, 300, 0] = float("inf")
+    x[1, 301, 1] = float("-inf")
+    x[0, 400:405, :] = float("nan")
+    for xin in (x, x.to(torch.bfloat16)):
+        out, cn, mn = v10_chunked_ttt(xin.to(dev), c.to(dev), m.to(dev), n_heads=H)
+        torch.cuda.synchronize()
+        compare(out, cn, mn, oracle(xin.float(), c, m, n_heads=H))
+
+
+def test_v10_k_above_eight_passes_extra_coefficients_through(dev):
+    B, S, H, hd, K = 1, 300, 2, 16, 10
+    x, c, m = case(B, S, H, hd, K, seed=3, mom_scale=0.01)
+    out, cn, mn = v10_chunked_ttt(x.to(dev), c.to(dev), m.to(dev), n_heads=H)
+    torch.cuda.synchronize()
+    assert torch.equal(cn[:, :, 8:].cpu(), c[:, :, 8:]) and torch.equal(mn[:, :, 8:].cpu(), m[:, :, 8:])
+    wo, wc, wm = oracle(x, c[:, :, :8], m[:, :, :8], n_heads=H)
+    compare(out, cn[:, :, :8], mn[:, :, :8], (wo, wc, wm))
+
+
+def test_v10_saved_z_and_coefficient_history(dev):
+    B, S, H, hd, K = 2, 600, 4, 16, 8
+    x, c, m = case(B, S, H, hd, K, seed=13)
+    out, cn, mn, z, hist = v10_chunked_ttt(x.to(dev), c.to(dev), m.to(dev), n_heads=H, save_for_backward=True)
+    torch.cuda.synchronize()
+    assert z.dtype == torch.bfloat16 and hist.shape == (3, B, H, K, hd)
+    assert torch.equal(hist[0].cpu(), c)
+    xb = V.bf16_round(x.numpy())
+    cc, mm = c.double().numpy(), m.double().numpy()
+    for ch in range(3):
+        np.testing.assert_allclose(hist[ch].cpu().numpy(), cc, rtol=1e-5, atol=1e-6)
+        s, cc, mm, zz = V.v10_chunk(xb[:, ch * 256:(ch + 1) * 256], cc, mm, ema_momentum=0.9, base_lr=0.005,
+                                    beta1=0.9, beta2=0.99, wd=0.01)
+        got = z[:, ch * 256:(ch + 1) * 256].float().cpu().numpy()
+        assert np.abs(got - zz).max() <= 8e-3          # bf16 storage of z
+
+
+def test_v10_is_deterministic(dev):
+    x, c, m = case(2, 900, 4, 16, 8, seed=17)
+    a = v10_chunked_ttt(x.to(dev), c.to(dev), m.to(dev), n_heads=4)
+    b = v10_chunked_ttt(x.to(dev), c.to(dev), m.to(dev), n_heads=4)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+def test_dropin_full_path(dev):
+    B, S, H, hd, K = 2, 800, 4, 16, 8
+    x, c, m = case(B, S, H, hd, K, seed=21)
+    gate = torch.tensor([0.7, 1.2])
+    out, cn, mn = apply_cheby_rkv_v10(x.to(dev), c.to(dev), m.to(dev), n_heads=H, seq_threshold=384,
+                                      gate_global=gate.to(dev), dynamic_lambda=gate.to(dev))
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32 and cn.dtype == torch.float32
+    compare(out, cn, mn, oracle(x, c, m, n_heads=H, gate_global=gate.numpy(), dynamic_lambda=gate.numpy()))
+    # below the threshold the same call takes the fixed-coefficient path
+    out_s, c_s, m_s = apply_cheby_rkv_v10(x[:, :300].to(dev), c.to(dev), m.to(dev), n_heads=H, seq_threshold=384)
+    assert torch.equal(c_s.cpu(), c)
