@@ -81,6 +81,10 @@ typedef enum osm_status {
 #define OSM_FLAG_NAN_ZERO_U 0x2 /* a NaN x counts as u = 0 (the reference's PyTorch
                                    fast path, sdpc_kernel.py:1725) instead of
                                    giving z = 0 (its Triton kernels, 2086) */
+#define OSM_FLAG_FULL_JACOBIAN 0x4 /* osm_cheby_ema_bwd only: dL/dx uses 1/(1+|x|)^2
+                                      everywhere (NaN where x is NaN), as the
+                                      full path's backward (sdpc_kernel.py:2505),
+                                      instead of 0 where |x| < 1e-7 or NaN */
 
 /* TTT target y */
 typedef enum osm_ttt_target { OSM_TARGET_X = 0, OSM_TARGET_SOFTSIGN = 1 } osm_ttt_target;
@@ -140,6 +144,11 @@ typedef struct osm_cheby_bwd_args {
   int64_t gx_stride_b, gx_stride_s;
   float* grad_coeffs;       /* optional [B,H,K,hd] fp32 contiguous (overwritten) */
   float* grad_init;         /* optional [B, H*hd] fp32 contiguous: dL/d ema_init */
+  const void* z_saved;      /* optional [B,S,H*hd] bf16: z of the forward (osm_v10_args.z_save);
+                               1 - z^2 is then taken from it instead of recomputed, as the
+                               full path's backward does (sdpc_kernel.py:2479-2481).
+                               Static lambda and an fp32 out only. */
+  int64_t z_stride_b, z_stride_s;
 } osm_cheby_bwd_args;
 
 /*

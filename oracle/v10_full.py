@@ -214,3 +214,59 @@ def v10_full(x, coeffs, momentum, *, n_heads=4, base_lr=0.005, ema_momentum=0.9,
                                use_lut=use_lut, lut=lut)
         outs.append(bf16_round(s.astype(np.float32)))
     return np.concatenate(outs, axis=1), c, m
+
+
+def v10_backward(x, out, zb, hist, grad_out, *, n_heads, ema_momentum, chunk):
+    """The reference's backward of the full path (FusedChebyRKVv10.backward,
+    sdpc_kernel.py:2436-2515) applied to every chunk (the chunk loop,
+    2583-2603, feeds each chunk its own coefficients; the EMA and its adjoint
+    restart at every chunk):
+
+        u      = sign(x) (1 - 1/(1 + max(|x|, 1e-7))), NaN -> 0     (2450-2453, fp32 x)
+        a[t]   = m[t] (dL/dout[t] + mu a[t+1]), a = 0 past the chunk, m = [|out| < 1 - 1e-6]
+        dL/dy  = (1 - mu) a (1 - zb^2)           zb: the forward's bf16 z   (879-881)
+        dL/dc_k = sum_t gamma dL/dy T_k(u)                                  (883-913)
+        dL/dx  = dL/dy gamma sum_k k c_k U_{k-1}(u) / (1 + |x|)^2           (923-961, 2505)
+
+    hist: [n_chunks, B, H, K, hd] coefficients each chunk used.  Returns
+    (grad_x [B,S,D], grad_coeffs of the first chunk [B,H,K,hd])."""
+    x = np.asarray(x, dtype=np.float64)
+    B, S, D = x.shape
+    n_chunks, _, H, K, hd = np.shape(hist)
+    mu = float(ema_momentum)
+    nan = np.isnan(x)
+    xs = np.where(nan, 0.0, x)
+    ax = np.maximum(np.abs(xs), np.float64(np.float32(1e-7)))
+    u = np.where(nan, 0.0, np.sign(xs) * (1.0 - 1.0 / (1.0 + ax)))
+    bound = float(np.float32(1.0 - 1e-6))
+    m = np.abs(np.asarray(out, np.float64)) < bound
+    g = np.asarray(grad_out, np.float64)
+    zb = np.asarray(zb, np.float64)
+    gamma = np.repeat(0.98 - 0.06 * np.arange(H) / H, hd)
+    gx = np.zeros_like(x)
+    gc0 = None
+    for ch in range(n_chunks):
+        t0, t1 = ch * chunk, min((ch + 1) * chunk, S)
+        adj = np.zeros((B, t1 - t0, D))
+        acc = np.zeros((B, D))
+        for t in range(t1 - 1, t0 - 1, -1):
+            acc = np.where(m[:, t], g[:, t] + mu * acc, 0.0)
+            adj[:, t - t0] = acc
+        dldy = (1.0 - mu) * adj * (1.0 - zb[:, t0:t1] ** 2)
+        uc = u[:, t0:t1]
+        T = [np.ones_like(uc), uc]
+        for _ in range(2, K):
+            T.append(2.0 * uc * T[-1] - T[-2])
+        gc = np.stack([np.sum(gamma * dldy * T[k], axis=1) for k in range(K)], axis=-1)   # [B,D,K]
+        if ch == 0:
+            gc0 = gc.reshape(B, H, hd, K).transpose(0, 1, 3, 2)
+        cl = np.asarray(hist[ch], np.float64).transpose(0, 1, 3, 2).reshape(B, 1, D, K)
+        U = [np.ones_like(uc), 2.0 * uc]
+        for _ in range(2, K):
+            U.append(2.0 * uc * U[-1] - U[-2])
+        dp = np.zeros_like(uc)
+        for k in range(1, K):
+            dp += k * cl[..., k] * U[k - 1]
+        with np.errstate(invalid="ignore"):
+            gx[:, t0:t1] = dldy * gamma * dp / (1.0 + np.abs(x[:, t0:t1])) ** 2
+    return gx, gc0

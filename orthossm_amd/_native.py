@@ -18,6 +18,7 @@ F32 = 0
 BF16 = 1
 FLAG_NO_CLAMP = 0x1
 FLAG_NAN_ZERO_U = 0x2
+FLAG_FULL_JACOBIAN = 0x4
 TARGET_X = 0
 TARGET_SOFTSIGN = 1
 OP_FWD = 0
@@ -98,6 +99,9 @@ class BwdArgs(ctypes.Structure):
         ("gx_stride_s", ctypes.c_int64),
         ("grad_coeffs", ctypes.c_void_p),
         ("grad_init", ctypes.c_void_p),
+        ("z_saved", ctypes.c_void_p),
+        ("z_stride_b", ctypes.c_int64),
+        ("z_stride_s", ctypes.c_int64),
     ]
 
 

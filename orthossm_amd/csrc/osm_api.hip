@@ -47,8 +47,8 @@ int check_args(const osm_cheby_args* a, Geometry* geo, int op, bool shapes_only 
   if (!a) return fail(OSM_E_ARG, "args is NULL");
   if (a->abi_version != OSM_ABI_VERSION)
     return fail(OSM_E_ARG, "abi_version %d does not match library ABI %d", a->abi_version, OSM_ABI_VERSION);
-  if (a->flags & ~(OSM_FLAG_NO_CLAMP | OSM_FLAG_NAN_ZERO_U))
-    return fail(OSM_E_ARG, "unknown flag bits 0x%x", a->flags);
+  const int known = OSM_FLAG_NO_CLAMP | OSM_FLAG_NAN_ZERO_U | (op == OSM_OP_BWD ? OSM_FLAG_FULL_JACOBIAN : 0);
+  if (a->flags & ~known) return fail(OSM_E_ARG, "unknown flag bits 0x%x", a->flags);
   if (a->B < 0 || a->S < 0) return fail(OSM_E_SHAPE, "B=%lld and S=%lld must be >= 0", (long long)a->B, (long long)a->S);
   if (a->H < 1 || a->hd < 4 || a->hd % 4 != 0)
     return fail(OSM_E_SHAPE, "need H >= 1 and hd a positive multiple of 4 (H=%lld hd=%lld)", (long long)a->H,
@@ -428,6 +428,13 @@ int osm_cheby_ema_bwd(const osm_cheby_args* args, const osm_cheby_bwd_args* bwd,
   if ((tile_rows * bwd->go_stride_s + D) * os >= (int64_t(1) << 31) ||
       (tile_rows * bwd->gx_stride_s + D) * xs >= (int64_t(1) << 31))
     return fail(OSM_E_LAYOUT, "token stride too large for 31-bit tile offsets");
+  if (bwd->z_saved) {
+    if (geo.dyn || args->out_dtype != OSM_F32)
+      return fail(OSM_E_ARG, "z_saved needs a static lambda and an fp32 out");
+    if ((uintptr_t)bwd->z_saved % 2 || bwd->z_stride_b < 0 || bwd->z_stride_s < 0 ||
+        (tile_rows * bwd->z_stride_s + D) * 2 >= (int64_t(1) << 31))
+      return fail(OSM_E_LAYOUT, "z_saved must be bf16-aligned with non-negative strides fitting 31-bit offsets");
+  }
   rc = check_ws(geo, OSM_OP_BWD, (int)args->K, workspace, workspace_bytes);
   if (rc != OSM_OK) return rc;
   // Only the header and look-back words need clearing: the partials are
@@ -447,6 +454,10 @@ int osm_cheby_ema_bwd(const osm_cheby_args* args, const osm_cheby_bwd_args* bwd,
   bp.grad_state = bwd->grad_state;
   bp.grad_init = bwd->grad_init;
   bp.grad_coeffs = bwd->grad_coeffs;
+  bp.zs = bwd->z_saved;
+  bp.zs_sb = bwd->z_stride_b;
+  bp.zs_ss = bwd->z_stride_s;
+  bp.full_jac = (args->flags & OSM_FLAG_FULL_JACOBIAN) ? 1 : 0;
   const hipError_t e = osm::launch_bwd(bp, args->x_dtype, args->out_dtype, geo.dyn, geo.tile, geo.kpad, st);
   if (e != hipSuccess) return hip_fail(e, "backward kernel launch");
   return ok();

@@ -92,12 +92,15 @@ __device__ __forceinline__ void accumulate_basis(float (&Gk)[KP], float e, float
 // y' times 2 ln2 (and 1 - lam for a static lambda).  SLOW handles, per
 // element, tokens >= S (r >= n_valid: identity map, no contribution), the clamp mask
 // (mbits bit r set: m = 0), NaN inputs (u = 0; e = 0 unless nan_zero_u);
-// the fast variant assumes none of them occurs in the run.
-template <class G, bool DYN, bool SLOW, typename XT, int KP>
+// the fast variant assumes none of them occurs in the run.  ZS: 1 - z^2 comes
+// from the saved z (zv) instead of the recomputed series.  full_jac: dL/dx
+// uses 1/(1+|x|)^2 everywhere (NaN for a NaN x) instead of 0 below 1e-7.
+template <class G, bool DYN, bool SLOW, bool ZS, typename XT, int KP>
 __device__ __forceinline__ void bwd_pass2(float& v, float (&Gk)[KP], const float (&xv)[G::R], const float (&gv)[G::R],
-                                          const float (&lamv)[G::R], float lam_h, const float (&c)[KP],
-                                          const float (&dm)[KP > 1 ? KP - 1 : 1], const RowStream& gx,
-                                          int n_valid, unsigned mbits, bool nan_zero_u) {
+                                          const float (&zv)[ZS ? G::R : 1], const float (&lamv)[G::R], float lam_h,
+                                          const float (&c)[KP], const float (&dm)[KP > 1 ? KP - 1 : 1],
+                                          const RowStream& gx, int n_valid, unsigned mbits, bool nan_zero_u,
+                                          bool full_jac) {
   constexpr int R = G::R;
   uint32_t so = (uint32_t)(R - 1) * gx.s;
   asm volatile("" : "+s"(so));
@@ -117,14 +120,20 @@ __device__ __forceinline__ void bwd_pass2(float& v, float (&Gk)[KP], const float
     const float ir = __builtin_amdgcn_rcpf(1.0f + __builtin_fabsf(x));
     float u = __builtin_copysignf(1.0f - ir, x);
     if constexpr (SLOW) u = (x == x) ? u : 0.0f;
-    const float rr = tanh_r(horner<KP>(u, c));
-    float e = av * __builtin_fmaf(-rr, rr, rr);
+    float hq;   // r (1 - r) = (1 - z^2) / 4
+    if constexpr (ZS) {
+      hq = 0.25f * __builtin_fmaf(-zv[r], zv[r], 1.0f);
+    } else {
+      const float rr = tanh_r(horner<KP>(u, c));
+      hq = __builtin_fmaf(-rr, rr, rr);
+    }
+    float e = av * hq;
     if constexpr (DYN) e *= 1.0f - lam;
     if constexpr (SLOW) e = live ? e : 0.0f;
     float dy = 0.0f;
     if constexpr (KP > 1) dy = horner<KP - 1>(u, dm);
     float gxv[1] = {e * dy * ir * ir};
-    gxv[0] = __builtin_fabsf(x) >= kSoftsignGradMin ? gxv[0] : 0.0f;
+    if (!full_jac) gxv[0] = __builtin_fabsf(x) >= kSoftsignGradMin ? gxv[0] : 0.0f;
     BufVec<XT, 1>::store(gx.r, gx.v, so, gxv);
     if (r > 0) so = prev_off(so, gx.s);
     accumulate_basis<KP>(Gk, e, u);
@@ -132,7 +141,7 @@ __device__ __forceinline__ void bwd_pass2(float& v, float (&Gk)[KP], const float
 }
 
 // Two workgroups (4 waves per SIMD) per CU: at most 128 VGPRs.
-template <class G, bool DYN, typename XT, typename OT, int KP>
+template <class G, bool DYN, bool ZS, typename XT, typename OT, int KP>
 __global__ void __launch_bounds__(G::THREADS) __attribute__((amdgpu_waves_per_eu(4)))
 cheby_ema_bwd_kernel(const BwdParams bp) {
   constexpr int R = G::R;
@@ -247,6 +256,18 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
       so = next_off(so, a.sx);
     }
   }
+  float zv[ZS ? R : 1];
+  if constexpr (ZS) {
+    const RowStream zs = row_stream<G, __bf16>(bp.zs, bp.zs_sb, bp.zs_ss, p, q, tm);
+    uint32_t so = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float t[1];
+      BufVec<__bf16, 1>::load(zs.r, zs.v, so, t);
+      zv[r] = t[0];
+      so = next_off(so, zs.s);
+    }
+  }
 
   const LaneSlots ls = lane_slots<G, true>(p.slots, ti, p.n_tiles);
   float pA, pB[1], aggA, aggB;
@@ -277,10 +298,13 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
   bool bad = false;
 #pragma unroll
   for (int r = 0; r < R; ++r) bad |= xv[r] != xv[r];
+  const bool full_jac = bp.full_jac != 0;
   if (slow1 || bad)
-    bwd_pass2<G, DYN, true, XT, KP>(v, Gk, xv, gv, lamv, lam_h, c[0], dm, gx, n_valid, mbits, p.nan_zero_u != 0);
+    bwd_pass2<G, DYN, true, ZS, XT, KP>(v, Gk, xv, gv, zv, lamv, lam_h, c[0], dm, gx, n_valid, mbits,
+                                        p.nan_zero_u != 0, full_jac);
   else
-    bwd_pass2<G, DYN, false, XT, KP>(v, Gk, xv, gv, lamv, lam_h, c[0], dm, gx, n_valid, 0u, false);
+    bwd_pass2<G, DYN, false, ZS, XT, KP>(v, Gk, xv, gv, zv, lamv, lam_h, c[0], dm, gx, n_valid, 0u, false,
+                                         full_jac);
 
   // dL/d ema_init = v[0], held by the first run of tile 0.
   if (tm.tile == 0 && q.tg == 0 && bp.grad_init) {
@@ -333,11 +357,11 @@ __global__ void __launch_bounds__(kRedSlices * kLanes) bwd_reduce(const float* p
   grad[(((size_t)b * H + h) * K + k) * hd + j] = sum * scale;
 }
 
-template <class G, bool DYN, typename XT, typename OT, int KP>
+template <class G, bool DYN, bool ZS, typename XT, typename OT, int KP>
 hipError_t launch_all(const BwdParams& bp, hipStream_t stream) {
   const FwdParams& p = bp.f;
   const unsigned grid = (unsigned)p.n_lb_pad * (unsigned)p.n_tiles;
-  hipLaunchKernelGGL((cheby_ema_bwd_kernel<G, DYN, XT, OT, KP>), dim3(grid), dim3(G::THREADS), 0, stream, bp);
+  hipLaunchKernelGGL((cheby_ema_bwd_kernel<G, DYN, ZS, XT, OT, KP>), dim3(grid), dim3(G::THREADS), 0, stream, bp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !bp.grad_coeffs) return e;
   hipLaunchKernelGGL((bwd_reduce<KP>), dim3(KP, p.n_lb), dim3(kRedSlices * kLanes), 0, stream, p.partials,
@@ -349,8 +373,16 @@ template <bool DYN, typename XT, typename OT>
 hipError_t launch_k(const BwdParams& bp, int tile, int kpad, hipStream_t stream) {
   using G = BwdTile;
   if (tile != G::TILE) return hipErrorInvalidValue;
-  if (kpad == 4) return launch_all<G, DYN, XT, OT, 4>(bp, stream);
-  return launch_all<G, DYN, XT, OT, 8>(bp, stream);
+  if (bp.zs) {
+    // Saved z (the full path's backward): static lambda and an fp32 output only.
+    if constexpr (!DYN && std::is_same<OT, float>::value) {
+      if (kpad == 4) return launch_all<G, false, true, XT, OT, 4>(bp, stream);
+      return launch_all<G, false, true, XT, OT, 8>(bp, stream);
+    }
+    return hipErrorInvalidValue;
+  }
+  if (kpad == 4) return launch_all<G, DYN, false, XT, OT, 4>(bp, stream);
+  return launch_all<G, DYN, false, XT, OT, 8>(bp, stream);
 }
 
 template <bool DYN>

@@ -117,6 +117,9 @@ struct BwdParams {
   const float* grad_state;     // dL/d ema_final [B,D] or NULL
   float* grad_init;            // dL/d ema_init [B,D] or NULL
   float* grad_coeffs;          // [B,H,K,hd]
+  const void* zs;              // saved z, bf16 [B,S,D], or NULL (recompute)
+  int64_t zs_sb, zs_ss;
+  int full_jac;                // dL/dx with 1/(1+|x|)^2 everywhere (no 1e-7 cutoff)
 };
 
 // Full-path launch (online TTT over chunks with an inline Lion update): one

@@ -193,7 +193,8 @@ def cheby_ema_backward(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, out:
                        lam_min: float = 0.9, lam_max: float = 0.9999, grad_state: torch.Tensor | None = None,
                        clamp: bool = True, nan_policy: str = "zero_z", need_coeffs: bool = True,
                        need_init: bool = False, grad_x_out: torch.Tensor | None = None,
-                       grad_coeffs_out: torch.Tensor | None = None, grad_init_out: torch.Tensor | None = None):
+                       grad_coeffs_out: torch.Tensor | None = None, grad_init_out: torch.Tensor | None = None,
+                       z_saved: torch.Tensor | None = None, full_jacobian: bool = False):
     """Backward of ``cheby_ema_forward``.
 
     ``out`` is the saved forward output (its clamp mask |out| < 1 - 1e-6
@@ -203,7 +204,10 @@ def cheby_ema_backward(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, out:
     grad_coeffs [B,H,K,hd] fp32 or None, grad_init [B,D] fp32 or None).
     lambda and damping are treated as constants.  ``grad_x_out``,
     ``grad_coeffs_out`` and ``grad_init_out`` (contiguous, on the device)
-    receive the results instead of new tensors.
+    receive the results instead of new tensors.  ``z_saved`` (bf16 [B,S,D],
+    the forward's z) makes the backward take 1 - z^2 from it, and
+    ``full_jacobian`` uses 1/(1+|x|)^2 everywhere, as the reference's
+    full-path backward does.
     """
     lib = nat.load()
     if out is None and clamp:
@@ -246,6 +250,12 @@ def cheby_ema_backward(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, out:
     bw.grad_x, bw.gx_stride_b, bw.gx_stride_s = gx.data_ptr(), gx.stride(0), gx.stride(1)
     bw.grad_coeffs = gc.data_ptr() if gc is not None else None
     bw.grad_init = gi.data_ptr() if gi is not None else None
+    if z_saved is not None:
+        if tuple(z_saved.shape) != (B, S, D) or z_saved.dtype != torch.bfloat16 or z_saved.stride(2) != 1:
+            raise ValueError("z_saved must be a bf16 [B,S,D] tensor with a contiguous lane dimension")
+        bw.z_saved, bw.z_stride_b, bw.z_stride_s = z_saved.data_ptr(), z_saved.stride(0), z_saved.stride(1)
+    if full_jacobian:
+        a.flags |= nat.FLAG_FULL_JACOBIAN
     stream = torch.cuda.current_stream(dev).cuda_stream
     nbytes = lib.osm_workspace_bytes(ctypes.byref(a), nat.OP_BWD)
     if nbytes == 0:
@@ -417,6 +427,93 @@ def v10_chunked_ttt(x: torch.Tensor, coeffs: torch.Tensor, momentum: torch.Tenso
     if save_for_backward:
         return out, c_out, m_out, z, hist
     return out, c_out, m_out
+
+
+def _v10_backward(x, out, z, hist, grad_out, n_heads, ema_momentum, chunk, need_coeffs):
+    """The full path's backward (FusedChebyRKVv10.backward, sdpc_kernel.py:
+    2436-2515) on every chunk: the adjoint restarts at each chunk end, the
+    chunk's own coefficients enter, 1 - z^2 comes from the saved bf16 z, the
+    mask from the output, dL/dx = ... / (1+|x|)^2.  Chunks become batch rows
+    of one backward call (per batch row when S is not a multiple of chunk).
+    Returns (grad_x, grad_coeffs of the first chunk or None)."""
+    B, S, D = x.shape
+    n_chunks, _, H, K, hd = hist.shape
+    dev = x.device
+    h = torch.arange(H, dtype=torch.float32, device=dev)
+    damping = (0.98 - 0.06 * h / H).contiguous()
+    lam = torch.full((H,), float(ema_momentum), dtype=torch.float32, device=dev)
+    go = grad_out.to(dtype=torch.float32).contiguous()
+    xc = x.contiguous()
+    gx = torch.empty_like(xc)
+    kw = dict(clamp=True, nan_policy="zero_u", need_coeffs=False, full_jacobian=True)
+    n_full = S // chunk
+    if n_chunks == 1:
+        gxa, gca, _ = cheby_ema_backward(xc, hist[0], damping, lam, out, go, z_saved=z,
+                                         **dict(kw, need_coeffs=need_coeffs))
+        return gxa, gca
+    def rows(t, b0, b1, nc):
+        return t[b0:b1, :nc * chunk].reshape((b1 - b0) * nc, chunk, D)
+    if S % chunk == 0:
+        cs = hist.permute(1, 0, 2, 3, 4).reshape(B * n_chunks, H, K, hd)
+        gxa, _, _ = cheby_ema_backward(rows(xc, 0, B, n_chunks), cs, damping, lam, rows(out, 0, B, n_chunks),
+                                       rows(go, 0, B, n_chunks), z_saved=rows(z, 0, B, n_chunks), **kw)
+        return gxa.reshape(B, S, D), None
+    for b in range(B):
+        gxa, _, _ = cheby_ema_backward(rows(xc, b, b + 1, n_full), hist[:n_full, b].contiguous(), damping, lam,
+                                       rows(out, b, b + 1, n_full), rows(go, b, b + 1, n_full),
+                                       z_saved=rows(z, b, b + 1, n_full), **kw)
+        gx[b, :n_full * chunk] = gxa.reshape(n_full * chunk, D)
+    t0 = n_full * chunk
+    gxt, _, _ = cheby_ema_backward(xc[:, t0:], hist[n_full], damping, lam, out[:, t0:], go[:, t0:],
+                                   z_saved=z[:, t0:], **kw)
+    gx[:, t0:] = gxt
+    return gx, None
+
+
+class _V10FullFn(torch.autograd.Function):
+    """The full path with the reference's backward: dL/dx always, dL/dc when
+    the sequence is one chunk (the chunk loop detaches the coefficients,
+    sdpc_kernel.py:2593-2594)."""
+
+    @staticmethod
+    def forward(ctx, x, coeffs, momentum, kw):
+        out, c_new, m_new, z, hist = v10_chunked_ttt(x, coeffs, momentum, save_for_backward=True, **kw)
+        ctx.save_for_backward(x, out, z, hist)
+        ctx.kw = kw
+        ctx.c_meta = (coeffs.dtype, coeffs.shape)
+        return out, c_new, m_new
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_c_new, grad_m_new):
+        x, out, z, hist = ctx.saved_tensors
+        kw = ctx.kw
+        need_c = ctx.needs_input_grad[1] and hist.shape[0] == 1
+        if grad_out is None:
+            grad_out = torch.zeros_like(out)
+        gx, gc = _v10_backward(x, out, z, hist, grad_out, kw["n_heads"], kw["ema_momentum"],
+                               min(kw["chunk_size"], x.shape[1]), need_c)
+        gx = gx.to(x.dtype) if ctx.needs_input_grad[0] else None
+        if need_c:
+            dt, shape = ctx.c_meta
+            if shape[2] > gc.shape[2]:
+                gc = torch.cat([gc, gc.new_zeros(shape[0], shape[1], shape[2] - gc.shape[2], shape[3])], dim=2)
+            gc = gc.to(dt)
+        else:
+            gc = None
+        return gx, gc, None, None
+
+
+def v10_full_path(x, coeffs, momentum, *, n_heads: int, base_lr: float = 0.005, ema_momentum: float = 0.9,
+                  beta1: float = 0.9, beta2: float = 0.99, weight_decay: float = 0.01, chunk_size: int = 256,
+                  gate_global=None, dynamic_lambda=None, use_lut: bool = True):
+    """``v10_chunked_ttt`` as a differentiable op with the reference's
+    backward of the full path.  Returns (out, coeffs_new, momentum_new)."""
+    kw = dict(n_heads=n_heads, base_lr=base_lr, ema_momentum=ema_momentum, beta1=beta1, beta2=beta2,
+              weight_decay=weight_decay, chunk_size=chunk_size, gate_global=gate_global,
+              dynamic_lambda=dynamic_lambda, use_lut=use_lut)
+    if x.dim() == 3 and x.shape[1] > chunk_size:
+        coeffs = coeffs.detach()
+    return _V10FullFn.apply(x, coeffs, momentum, kw)
 
 
 def _check_dest(t: torch.Tensor, shape, dev, name: str) -> None:

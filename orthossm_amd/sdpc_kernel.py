@@ -20,14 +20,15 @@ The full path (``S >= seq_threshold``; sdpc_kernel.py:2559-2606: online TTT
 over ``chunk_size``-token chunks, each a ``FusedChebyRKVv10.forward`` with the
 inline Lion update, LUT or 4-term Clenshaw series, clamped tanh, EMA restarted
 at every chunk, bf16 rounding of x and of the output) runs as one launch of
-``v10_chunked_ttt``.  Gradients through the full path are not covered yet and
-raise ``NotImplementedError``.
+``v10_chunked_ttt``; with gradients enabled, through ``v10_full_path``,
+whose backward is the reference's (FusedChebyRKVv10.backward,
+sdpc_kernel.py:2436-2515) on every chunk.
 """
 from __future__ import annotations
 
 import torch
 
-from .ops import cheby_ema, cheby_ema_forward, v10_chunked_ttt
+from .ops import cheby_ema, cheby_ema_forward, v10_chunked_ttt, v10_full_path
 
 
 def v10_damping(n_heads: int, device=None) -> torch.Tensor:
@@ -51,9 +52,10 @@ def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_m
     if D % H:
         raise ValueError(f"D={D} is not divisible by n_heads={H}")
     if not (seq_threshold > 0 and S < seq_threshold):
+        run = v10_chunked_ttt
         if torch.is_grad_enabled() and (x.requires_grad or coeffs.requires_grad):
-            raise NotImplementedError("orthossm_amd: gradients through the full path are not implemented yet")
-        out, c_new, m_new = v10_chunked_ttt(
+            run = v10_full_path
+        out, c_new, m_new = run(
             x, coeffs, momentum_buf, n_heads=H, base_lr=base_lr, ema_momentum=ema_momentum, beta1=lion_beta1,
             beta2=lion_beta2, weight_decay=lion_wd, chunk_size=chunk_size, gate_global=gate_global,
             dynamic_lambda=dynamic_lambda, use_lut=use_lut)

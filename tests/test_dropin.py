@@ -20,10 +20,10 @@ def test_full_path_needs_the_gpu_and_a_momentum_buffer():
         apply_cheby_rkv_v10(x, c, None, n_heads=4, seq_threshold=0)
 
 
-def test_full_path_gradients_raise():
+def test_full_path_gradients_need_the_gpu_too():
     x = torch.zeros(1, 512, 64, requires_grad=True)
     c = torch.zeros(1, 4, 4, 16)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="ROCm GPU only"):
         apply_cheby_rkv_v10(x, c, torch.zeros_like(c), n_heads=4, seq_threshold=384)
 
 

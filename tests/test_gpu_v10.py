@@ -132,3 +132,49 @@ def test_dropin_full_path(dev):
     # below the threshold the same call takes the fixed-coefficient path
     out_s, c_s, m_s = apply_cheby_rkv_v10(x[:, :300].to(dev), c.to(dev), m.to(dev), n_heads=H, seq_threshold=384)
     assert torch.equal(c_s.cpu(), c)
+
+
+def _grads_vs_oracle(dev, B, S, H, hd, K, chunk, seed, nan=False):
+    x, c, m = case(B, S, H, hd, K, seed=seed, mom_scale=0.01)
+    if nan:
+        x[0, 5, 2] = float("nan")
+    go = torch.randn(B, S, H * hd, generator=torch.Generator().manual_seed(seed + 1))
+    xd = x.to(dev).requires_grad_(True)
+    cd = c.to(dev).requires_grad_(True)
+    out, cn, mn = apply_cheby_rkv_v10(xd, cd, m.to(dev), n_heads=H, chunk_size=chunk, seq_threshold=0)
+    (out * go.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    # the oracle backward on the GPU forward's saved tensors
+    _, _, _, z, hist = v10_chunked_ttt(x.to(dev), c.to(dev), m.to(dev), n_heads=H, chunk_size=chunk,
+                                       save_for_backward=True)
+    wx, wc = V.v10_backward(x.numpy(), out.detach().cpu().numpy(), z.float().cpu().numpy(),
+                            hist.cpu().numpy(), go.numpy(), n_heads=H, ema_momentum=0.9, chunk=chunk)
+    return xd.grad, cd.grad, wx, wc
+
+
+def _close(got, want, what):
+    g = got.cpu().numpy().astype(np.float64)
+    ok = np.isfinite(want)
+    assert np.array_equal(np.isnan(g), np.isnan(want)), f"{what}: NaN pattern differs"
+    scale = np.abs(want[ok]).max()
+    err = np.abs(g[ok] - want[ok])
+    assert err.max() <= 1e-3 * scale, f"{what}: max err {err.max():.3e} vs scale {scale:.3e}"
+    assert (err > 1e-3 * np.abs(want[ok]) + 1e-4 * scale).mean() == 0, what
+
+
+@pytest.mark.parametrize("B,S,H,hd,K,chunk", [
+    (2, 768, 4, 16, 8, 256),    # S a multiple of chunk: one backward call
+    (3, 600, 2, 32, 8, 256),    # partial last chunk: per-row calls + tail
+    (2, 1000, 4, 16, 4, 100),
+])
+def test_v10_full_path_grad_x(dev, B, S, H, hd, K, chunk):
+    gx, gc, wx, _ = _grads_vs_oracle(dev, B, S, H, hd, K, chunk, seed=B + S)
+    assert gc is None                           # the chunk loop detaches the coefficients
+    _close(gx, wx, "grad_x")
+
+
+def test_v10_single_chunk_grads_and_nan(dev):
+    gx, gc, wx, wc = _grads_vs_oracle(dev, 2, 200, 4, 16, 8, 256, seed=77, nan=True)
+    assert torch.isnan(gx[0, 5, 2])
+    _close(gx, wx, "grad_x")
+    _close(gc, wc, "grad_coeffs")

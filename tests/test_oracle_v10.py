@@ -177,3 +177,42 @@ def test_full_path_chains_coefficients_over_chunks():
     o1, c1, _ = V.v10_full(x[:, :20], c, m, n_heads=H, chunk_size=32)
     s1, c1b, _, _ = V.v10_chunk(xb[:, :20], c, m, **KW)
     np.testing.assert_array_equal(c1, c1b)
+
+
+def test_full_path_backward_reduces_to_the_pinned_fast_path_backward():
+    # With zb = the exact tanh of the exact series (no LUT, no bf16, no +-4
+    # clamp binding) each chunk's backward is the fast-path backward of
+    # oracle/cheby_ema.py (pinned by autograd and finite differences) with
+    # damping gamma_h, lambda mu on every head, no state gradient.
+    from oracle import cheby_ema as O
+    B, S, H, hd, K, chunk = 2, 70, 2, 4, 8, 32
+    x = rng.standard_normal((B, S, H * hd))
+    hist = rng.standard_normal((3, B, H, K, hd)) / np.arange(1, K + 1).reshape(1, 1, 1, K, 1) * 0.5
+    go = rng.standard_normal((B, S, H * hd))
+    gamma = 0.98 - 0.06 * np.arange(H) / H
+    mu = 0.9
+    outs, zs = [], []
+    for ch in range(3):
+        t0, t1 = ch * chunk, min((ch + 1) * chunk, S)
+        o, _, parts = O.forward(x[:, t0:t1], hist[ch], gamma, np.full(H, mu), return_parts=True)
+        outs.append(o)
+        zs.append(parts["z"])
+    out, z = np.concatenate(outs, axis=1), np.concatenate(zs, axis=1)
+    gx, gc = V.v10_backward(x, out, z, hist, go, n_heads=H, ema_momentum=mu, chunk=chunk)
+    for ch in range(3):
+        t0, t1 = ch * chunk, min((ch + 1) * chunk, S)
+        wx, wc, _ = O.backward(x[:, t0:t1], hist[ch], gamma, np.full(H, mu), go[:, t0:t1])
+        np.testing.assert_allclose(gx[:, t0:t1], wx, rtol=1e-9, atol=1e-13)
+        if ch == 0:
+            np.testing.assert_allclose(gc, wc, rtol=1e-9, atol=1e-13)
+
+
+def test_full_path_backward_nan_gives_nan_grad_x():
+    B, S, H, hd, K = 1, 10, 1, 4, 4
+    x = rng.standard_normal((B, S, H * hd))
+    x[0, 3, 1] = np.nan
+    hist = rng.standard_normal((1, B, H, K, hd))
+    gx, gc = V.v10_backward(x, np.zeros_like(x), np.zeros_like(x), hist, np.ones_like(x), n_heads=H,
+                            ema_momentum=0.9, chunk=256)
+    assert np.isnan(gx[0, 3, 1]) and np.isfinite(np.delete(gx.reshape(-1), 3 * 4 + 1)).all()
+    assert np.isfinite(gc).all()
