@@ -34,6 +34,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 from orthossm_amd import cheby_ema_backward, cheby_ema_forward, cheby_ema_ttt  # noqa: E402
+from orthossm_amd.ops import v10_chunked_ttt  # noqa: E402
 from orthossm_amd.synthetic import CONFIGS, make_config_inputs  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
@@ -57,6 +58,10 @@ def algorithmic_bytes(cfg) -> int:
     total += 2 * cfg.B * cfg.D * 4 * launches            # ema_init in, ema_final out per launch
     if cfg.ttt or cfg.bwd:
         total += cfg.B * cfg.H * cfg.K * cfg.hd * 4      # grad
+    if cfg.v10:
+        total += 3 * cfg.B * cfg.H * cfg.K * cfg.hd * 4  # momentum in, coeffs and momentum out
+        total -= 2 * cfg.B * cfg.D * 4 * launches        # no EMA state arguments
+        total += 8 * 256 * 4                             # LUT
     return total
 
 
@@ -71,7 +76,12 @@ def cpu_baseline(cfg):
     c = inp["coeffs"][0:1]
     S = min(cfg.S, 16384)
     x = x[:, :S].contiguous()
-    if cfg.bwd:
+    if cfg.v10:
+        from oracle import v10_full as V
+        xs1, cs1 = x[:, :S].numpy(), c.double().numpy()
+        run = lambda: V.v10_full(xs1, cs1, 0.0 * cs1, n_heads=cfg.H, chunk_size=cfg.v10)   # noqa: E731
+        what = "the full path restated in float64 numpy (oracle/v10_full.py), LUT series"
+    elif cfg.bwd:
         out, _ = RF.forward(x, c, inp["damping"], inp["lam"])
         go = torch.randn(x.shape, generator=torch.Generator().manual_seed(1))
         run = lambda: RF.backward(x, c, inp["damping"], inp["lam"], out, go)      # noqa: E731
@@ -134,7 +144,7 @@ def pmc_summary(fetch_path: str, write_path: str, workload: str) -> dict:
         rows = _counter_rows(path, counter)
         ours = [float(r["Counter_Value"]) * 1024 for r in rows
                 if any(k in r["Kernel_Name"] for k in ("cheby_ema_fwd_kernel", "cheby_ema_ttt_kernel",
-                                                       "cheby_ema_bwd_kernel"))]
+                                                       "cheby_ema_bwd_kernel", "v10_chunked_kernel"))]
         copies = [float(r["Counter_Value"]) * 1024 for r in rows if "copyBuffer" in r["Kernel_Name"]][-5:]
         if not ours or len(copies) < 5:
             raise SystemExit(f"pmc_summary: {path} lacks kernel or 5 calibration copies for {counter}")
@@ -212,9 +222,13 @@ def main():
         gxs = [torch.empty_like(x0) for _ in range(args.sets)]
         torch.cuda.synchronize()
 
+    mom = torch.zeros_like(c) if cfg.v10 else None
+
     def step(i):
         x, out = xs[i % args.sets], outs[i % args.sets]
-        if cfg.bwd:
+        if cfg.v10:
+            v10_chunked_ttt(x, c, mom, n_heads=cfg.H, chunk_size=cfg.v10)
+        elif cfg.bwd:
             cheby_ema_backward(x, c, damp, lam, out, gos[i % args.sets], g=g, grad_state=state0,
                                grad_x_out=gxs[i % args.sets], grad_coeffs_out=grad, grad_init_out=states[0])
         elif cfg.ttt:
@@ -265,7 +279,8 @@ def main():
 
     res = {
         "metric": METRIC if args.workload == "headline" else
-        f"Clenshaw+EMA {'backward ' if cfg.bwd else ''}tokens/s, workload {cfg.name}",
+        f"Clenshaw+EMA {'backward ' if cfg.bwd else ''}{'full path (online TTT + Lion) ' if cfg.v10 else ''}"
+        f"tokens/s, workload {cfg.name}",
         "value": tokens / (ms_per_step * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -282,6 +297,7 @@ def main():
                         f"{'bf16' if cfg.dtype == torch.bfloat16 else 'fp32'}"
                         f"{' dynamic-lambda' if cfg.dynamic else ''}{' +TTT-grad' if cfg.ttt else ''}"
                         f"{' backward (dL/dx, dL/dc, dL/d ema_init)' if cfg.bwd else ''}"
+                        f"{f' full path: chunks of {cfg.v10} with Lion, LUT series' if cfg.v10 else ''}"
                         f"{f' as {cfg.S // cfg.chunk} chunks with carry' if cfg.chunk else ''}",
             "B": cfg.B, "S": cfg.S, "D": cfg.D, "H": cfg.H, "K": cfg.K,
             "parallelism": "single GPU",

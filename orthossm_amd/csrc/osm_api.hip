@@ -376,7 +376,8 @@ int osm_v10_chunked_ttt(const osm_v10_args* a, void* stream) {
   p.K = (int)a->K;
   p.D = (int)D;
   p.chunk = (int)std::min<int64_t>(a->chunk, a->S);
-  p.n_lg = (int)((a->hd + osm::kV10Lanes - 1) / osm::kV10Lanes);
+  p.lanes = osm::v10_lanes(a->B, a->H, a->hd);
+  p.n_lg = (int)((a->hd + p.lanes - 1) / p.lanes);
   p.mu = a->ema_momentum;
   p.base_lr = a->base_lr;
   p.beta1 = a->beta1;

@@ -123,11 +123,13 @@ struct BwdParams {
 };
 
 // Full-path launch (online TTT over chunks with an inline Lion update): one
-// workgroup per (batch row, head, group of kV10Lanes lanes) walks the chunks in
-// order.  Needs no workspace.
-constexpr int kV10Lanes = 16;     // lanes per workgroup
+// workgroup per (batch row, head, group of `lanes` lanes) walks the chunks in
+// order.  Needs no workspace.  The chunks of a lane are sequential, so the
+// lanes are the only parallelism: 16 lanes per workgroup when that still
+// gives >= 512 workgroups, else 8 (v10_lanes).
 constexpr int kV10Groups = 32;    // token groups (runs) per 256-token block
 constexpr int kV10Run = 8;        // tokens per run
+int v10_lanes(int64_t B, int64_t H, int64_t hd);
 struct V10Params {
   const void* x;
   float* out;
@@ -146,6 +148,7 @@ struct V10Params {
   int64_t x_sb, x_ss, o_sb, o_ss, z_sb, z_ss;
   int64_t c_sb, c_sh, c_sk, m_sb, m_sh, m_sk;
   int B, S, H, hd, K, D, chunk, n_lg;
+  int lanes;                   // lanes per workgroup (8 or 16)
   float mu, base_lr, beta1, beta2, wd;
 };
 

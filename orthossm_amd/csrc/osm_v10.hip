@@ -14,11 +14,11 @@
 //   gv = err / (1 + exp(-3|err|)), err = u_{t+1} - s_t; then Lion on (c, m).
 //
 // Chunks depend on each other only through (c, m) of each lane, so one
-// workgroup owns kV10Lanes lanes of one (batch row, head) and walks the
+// workgroup owns LW lanes of one (batch row, head) and walks the
 // chunks in order; the dependency never leaves the workgroup.  A chunk is
 // processed in 256-token blocks: thread (group g, lane l) owns a run of
 // kV10Run tokens; runs are composed by a scan in LDS; the proxy-gradient
-// sums are reduced over the runs in a fixed order, and kV10Lanes * K threads
+// sums are reduced over the runs in a fixed order, and LW * K threads
 // apply Lion and publish the next chunk's coefficients through LDS.
 #include "osm_tile.h"
 
@@ -26,7 +26,6 @@ namespace osm {
 namespace {
 
 constexpr int kBlockTok = kV10Groups * kV10Run;      // 256 tokens per block
-constexpr int kV10Threads = kV10Groups * kV10Lanes;  // 512
 constexpr float kLog2e = 1.4426950408889634f;
 
 // x rounded to bf16 (round to nearest even), as the reference casts on entry.
@@ -45,39 +44,41 @@ __device__ __forceinline__ float to_bf16_value<__bf16>(float v) {
 __device__ __forceinline__ void v10_softsign(float xb, float& absu, float& sgn) {
   const float xs = xb == xb ? xb : 0.0f;
   const float ax = __builtin_fmaxf(__builtin_fabsf(xs), 1e-7f);
-  absu = 1.0f - 1.0f / (1.0f + ax);
+  absu = 1.0f - __builtin_amdgcn_rcpf(1.0f + ax);
   sgn = xs >= 0.0f ? 1.0f : -1.0f;
 }
 
+template <int LW>
 struct V10Lds {
   float lut[256][8];                 // T_k at the table's grid, k contiguous
-  float cs[8][kV10Lanes];            // coefficients of the current chunk
-  float ms[8][kV10Lanes];            // Lion momentum
-  float aggA[kV10Groups][kV10Lanes];
-  float aggB[kV10Groups][kV10Lanes];
-  float u0[kV10Groups][kV10Lanes];   // u at each run's first token
-  float carry[kV10Lanes];            // EMA state entering the block
-  float gc[kV10Groups][8][kV10Lanes];
+  float cs[8][LW];                   // coefficients of the current chunk
+  float ms[8][LW];                   // Lion momentum
+  float aggA[kV10Groups][LW];
+  float aggB[kV10Groups][LW];
+  float carry[LW];                   // EMA state entering the block
+  float gc[kV10Groups][8][LW];
 };
 
-template <typename XT, int KP, bool LUT>
-__global__ void __launch_bounds__(kV10Threads) v10_chunked_kernel(const V10Params p) {
-  __shared__ V10Lds L;
+// LW lanes per workgroup (8 or 16), kV10Groups runs of kV10Run tokens each.
+template <typename XT, int KP, bool LUT, int LW>
+__global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10Params p) {
+  constexpr int kThreads = kV10Groups * LW;
+  __shared__ V10Lds<LW> L;
   const int tid = threadIdx.x;
-  const int l = tid % kV10Lanes, g = tid / kV10Lanes;
+  const int l = tid % LW, g = tid / LW;
   const int lg = blockIdx.x % p.n_lg;
   const int bh = blockIdx.x / p.n_lg;
   const int h = bh % p.H, b = bh / p.H;
-  const int j = lg * kV10Lanes + l;                 // lane inside the head
+  const int j = lg * LW + l;                 // lane inside the head
   const bool lane_ok = j < p.hd;
   const int d = h * p.hd + j;
 
   // Tables and the lanes' starting coefficients and momentum.
   if constexpr (LUT) {
-    for (int i = tid; i < 256 * 8; i += kV10Threads) L.lut[i % 256][i / 256] = p.lut[i];
+    for (int i = tid; i < 256 * 8; i += kThreads) L.lut[i % 256][i / 256] = p.lut[i];
   }
-  if (tid < KP * kV10Lanes) {
-    const int k = tid / kV10Lanes, ll = tid % kV10Lanes, jj = lg * kV10Lanes + ll;
+  if (tid < KP * LW) {
+    const int k = tid / LW, ll = tid % LW, jj = lg * LW + ll;
     const bool ok = jj < p.hd && k < p.K;
     L.cs[k][ll] = ok ? p.coeffs[(int64_t)b * p.c_sb + (int64_t)h * p.c_sh + (int64_t)k * p.c_sk + jj] : 0.0f;
     L.ms[k][ll] = ok ? p.momentum[(int64_t)b * p.m_sb + (int64_t)h * p.m_sh + (int64_t)k * p.m_sk + jj] : 0.0f;
@@ -94,12 +95,34 @@ __global__ void __launch_bounds__(kV10Threads) v10_chunked_kernel(const V10Param
   if (p.z_save)
     zr = make_rsrc(static_cast<const char*>(p.z_save) + (int64_t)b * p.z_sb * 2,
                    ((uint64_t)(p.S - 1) * p.z_ss + p.D) * 2);
-  const uint32_t vx = lane_ok ? (uint32_t)(d * sizeof(XT)) : kOffOOB;
-  const uint32_t vo = lane_ok ? (uint32_t)(d * 4) : kOffOOB;
-  const uint32_t vz = lane_ok ? (uint32_t)(d * 2) : kOffOOB;
+  const uint32_t x_row = (uint32_t)(p.x_ss * sizeof(XT));   // bytes per token
+  const uint32_t o_row = (uint32_t)(p.o_ss * 4);
+  const uint32_t z_row = (uint32_t)(p.z_ss * 2);
   __syncthreads();
 
+  // x rows of a run, double-buffered: the rows of the next block (or of the
+  // next chunk's first block) are in flight while this block computes.  A
+  // run also loads the row after it (the next run's first token, or the
+  // first token after the block), for the pair (t, t+1) of its last token.
+  // Rows past S read 0; rows past the chunk are loaded but not used.
   const int n_chunks = (p.S + p.chunk - 1) / p.chunk;
+  auto run_voff = [&](int t0) -> uint32_t {
+    return lane_ok ? (uint32_t)t0 * x_row + (uint32_t)(d * sizeof(XT)) : kOffOOB;
+  };
+  float xcur[kV10Run + 1], xnxt[kV10Run + 1];
+  auto load_run = [&](float (&dst)[kV10Run + 1], int t0) {
+    const uint32_t vo_ = run_voff(t0);
+    uint32_t so = 0;
+#pragma unroll
+    for (int r = 0; r <= kV10Run; ++r) {
+      float t[1];
+      BufVec<XT, 1>::load(xr, vo_, so, t);
+      dst[r] = t[0];
+      so = next_off(so, x_row);
+    }
+  };
+  load_run(xcur, g * kV10Run);
+
   for (int ch = 0; ch < n_chunks; ++ch) {
     const int t_chunk = ch * p.chunk;
     const int len = min(p.chunk, p.S - t_chunk);
@@ -113,32 +136,47 @@ __global__ void __launch_bounds__(kV10Threads) v10_chunked_kernel(const V10Param
     float gc[KP];
 #pragma unroll
     for (int k = 0; k < KP; ++k) gc[k] = 0.0f;
-    if (tid < kV10Lanes) L.carry[tid] = 0.0f;
+    if (tid < LW) L.carry[tid] = 0.0f;
 
     for (int blk = 0; blk * kBlockTok < len; ++blk) {
       const int r0 = blk * kBlockTok + g * kV10Run;      // run start inside the chunk
       const int n_valid = max(0, min(kV10Run, len - r0));
       const int t0 = t_chunk + r0;                        // run start in the sequence
-      float u[kV10Run], w[kV10Run];
+      // Prefetch the next block's rows.
+      int t_next = -1;
+      if ((blk + 1) * kBlockTok < len)
+        t_next = t_chunk + (blk + 1) * kBlockTok + g * kV10Run;
+      else if (ch + 1 < n_chunks)
+        t_next = t_chunk + p.chunk + g * kV10Run;
+      if (t_next >= 0) load_run(xnxt, t_next);
+
+      float u[kV10Run + 1], w[kV10Run];
       float A = 1.0f, Bv = 0.0f;
 #pragma unroll
-      for (int r = 0; r < kV10Run; ++r) {
-        float xv[1] = {0.0f};
-        if (r < n_valid) BufVec<XT, 1>::load(xr, vx, (uint32_t)((int64_t)(t0 + r) * p.x_ss * sizeof(XT)), xv);
-        const float xb = to_bf16_value<XT>(xv[0]);
+      for (int r = 0; r <= kV10Run; ++r) {
+        const float xb = to_bf16_value<XT>(xcur[r]);
         float absu, sgn;
         v10_softsign(xb, absu, sgn);
         u[r] = sgn * absu;
+        if (r == kV10Run) break;   // the row after the run: u only
         float y;
         if constexpr (LUT) {
           const float fidx = absu * 255.0f;
           const int i0 = min((int)fidx, 254);
           const float fr = __builtin_fminf(__builtin_fmaxf(fidx - (float)i0, 0.0f), 1.0f);
+          float ta[KP], tb[KP];
+          const f32x4* ra = reinterpret_cast<const f32x4*>(&L.lut[i0][0]);
+          const f32x4* rb = reinterpret_cast<const f32x4*>(&L.lut[i0 + 1][0]);
+#pragma unroll
+          for (int q4 = 0; q4 < KP / 4; ++q4) {
+            const f32x4 va = ra[q4], vb = rb[q4];
+            ta[4 * q4] = va.x; ta[4 * q4 + 1] = va.y; ta[4 * q4 + 2] = va.z; ta[4 * q4 + 3] = va.w;
+            tb[4 * q4] = vb.x; tb[4 * q4 + 1] = vb.y; tb[4 * q4 + 2] = vb.z; tb[4 * q4 + 3] = vb.w;
+          }
           float ye = 0.0f, yo = 0.0f;
 #pragma unroll
           for (int k = 0; k < KP; ++k) {
-            const float ta = L.lut[i0][k], tb = L.lut[i0 + 1][k];
-            const float it = __builtin_fmaf(fr, tb - ta, ta);
+            const float it = __builtin_fmaf(fr, tb[k] - ta[k], ta[k]);
             if (k & 1)
               yo = __builtin_fmaf(c[k], it, yo);
             else
@@ -147,14 +185,14 @@ __global__ void __launch_bounds__(kV10Threads) v10_chunked_kernel(const V10Param
           y = __builtin_fmaf(sgn, yo, ye);
         } else {
           const float uu = u[r], u2 = uu + uu;
-          const float c3 = KP > 3 ? c[3] : 0.0f, c2 = KP > 2 ? c[2] : 0.0f;
+          const float c3 = c[3], c2 = c[2];
           const float b2 = __builtin_fmaf(u2, c3, c2);
           const float b1 = __builtin_fmaf(u2, b2, c[1]) - c3;
           y = __builtin_fmaf(uu, b1, c[0]) - b2;
         }
         const float yc = __builtin_amdgcn_fmed3f(gamma * y, -4.0f, 4.0f);
         const float e2 = __builtin_amdgcn_exp2f(2.0f * kLog2e * yc);
-        float z = (e2 - 1.0f) / (e2 + 1.0f);
+        float z = (e2 - 1.0f) * __builtin_amdgcn_rcpf(e2 + 1.0f);
         z = xb == xb ? z : 0.0f;
         w[r] = one_m * z;
         if (r < n_valid) {
@@ -163,38 +201,27 @@ __global__ void __launch_bounds__(kV10Threads) v10_chunked_kernel(const V10Param
         }
         if (p.z_save && r < n_valid) {
           const float zz[1] = {z};
-          BufVec<__bf16, 1>::store(zr, vz, (uint32_t)((int64_t)(t0 + r) * p.z_ss * 2), zz);
+          BufVec<__bf16, 1>::store(zr, lane_ok ? (uint32_t)t0 * z_row + (uint32_t)(d * 2) : kOffOOB,
+                                   (uint32_t)r * z_row, zz);
         }
-      }
-      // u after the run: the next run's first token, or for the block's last
-      // run the first token after the block (inside the chunk).
-      float u_after = 0.0f;
-      if (g == kV10Groups - 1 && r0 + kV10Run < len) {
-        float xv[1];
-        BufVec<XT, 1>::load(xr, vx, (uint32_t)((int64_t)(t0 + kV10Run) * p.x_ss * sizeof(XT)), xv);
-        float absu, sgn;
-        v10_softsign(to_bf16_value<XT>(xv[0]), absu, sgn);
-        u_after = sgn * absu;
       }
       L.aggA[g][l] = A;
       L.aggB[g][l] = Bv;
-      L.u0[g][l] = u[0];
       __syncthreads();
       float s = L.carry[l];
       for (int q = 0; q < g; ++q) s = __builtin_fmaf(L.aggA[q][l], s, L.aggB[q][l]);
-      if (g < kV10Groups - 1) u_after = L.u0[g + 1][l];
       // Replay, store bf16(s), proxy gradient.
+      const uint32_t ovo = lane_ok ? (uint32_t)t0 * o_row + (uint32_t)(d * 4) : kOffOOB;
 #pragma unroll
       for (int r = 0; r < kV10Run; ++r) {
         if (r < n_valid) {
           s = __builtin_fmaf(mu, s, w[r]);
           const float so = __builtin_amdgcn_fmed3f(s, -1.0f, 1.0f);
           const float ov[1] = {(float)(__bf16)so};
-          BufVec<float, 1>::store(orr, vo, (uint32_t)((int64_t)(t0 + r) * p.o_ss * 4), ov);
+          BufVec<float, 1>::store(orr, ovo, (uint32_t)r * o_row, ov);
           if (r0 + r + 1 < len) {
-            const float un = r + 1 < kV10Run ? u[r + 1] : u_after;
-            const float err = un - so;
-            const float gv = err / (1.0f + __builtin_amdgcn_exp2f(-3.0f * kLog2e * __builtin_fabsf(err)));
+            const float err = u[r + 1] - so;
+            const float gv = err * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-3.0f * kLog2e * __builtin_fabsf(err)));
             const float uu = u[r], u2 = uu + uu;
             gc[0] += gv;
             if constexpr (KP > 1) gc[1] = __builtin_fmaf(gv, uu, gc[1]);
@@ -209,20 +236,22 @@ __global__ void __launch_bounds__(kV10Threads) v10_chunked_kernel(const V10Param
           }
         }
       }
-      __syncthreads();   // all reads of carry / aggregates / u0 done
+      __syncthreads();   // all reads of carry and the aggregates done
       if (g == kV10Groups - 1) {
         // state after the block's last valid token (invalid tokens are skipped)
         L.carry[l] = s;
       }
       __syncthreads();
+#pragma unroll
+      for (int r = 0; r <= kV10Run; ++r) xcur[r] = xnxt[r];
     }
 
     // Reduce the proxy gradient over the runs (fixed order), then Lion.
 #pragma unroll
     for (int k = 0; k < KP; ++k) L.gc[g][k][l] = gc[k];
     __syncthreads();
-    if (tid < KP * kV10Lanes) {
-      const int k = tid / kV10Lanes, ll = tid % kV10Lanes;
+    if (tid < KP * LW) {
+      const int k = tid / LW, ll = tid % LW;
       float G = 0.0f;
       for (int q = 0; q < kV10Groups; ++q) G += L.gc[q][k][ll];
       if (k < p.K) {
@@ -243,8 +272,8 @@ __global__ void __launch_bounds__(kV10Threads) v10_chunked_kernel(const V10Param
     __syncthreads();
   }
 
-  if (tid < KP * kV10Lanes) {
-    const int k = tid / kV10Lanes, ll = tid % kV10Lanes, jj = lg * kV10Lanes + ll;
+  if (tid < KP * LW) {
+    const int k = tid / LW, ll = tid % LW, jj = lg * LW + ll;
     if (jj < p.hd && k < p.K) {
       const size_t o = (((size_t)b * p.H + h) * p.K + k) * p.hd + jj;
       p.coeffs_out[o] = L.cs[k][ll];
@@ -253,17 +282,28 @@ __global__ void __launch_bounds__(kV10Threads) v10_chunked_kernel(const V10Param
   }
 }
 
-template <typename XT, bool LUT>
-hipError_t launch_x(const V10Params& p, int kpad, hipStream_t stream) {
+template <typename XT, bool LUT, int LW>
+hipError_t launch_w(const V10Params& p, int kpad, hipStream_t stream) {
   const unsigned grid = (unsigned)(p.B * p.H * p.n_lg);
   if (kpad == 4)
-    hipLaunchKernelGGL((v10_chunked_kernel<XT, 4, LUT>), dim3(grid), dim3(kV10Threads), 0, stream, p);
+    hipLaunchKernelGGL((v10_chunked_kernel<XT, 4, LUT, LW>), dim3(grid), dim3(kV10Groups * LW), 0, stream, p);
   else
-    hipLaunchKernelGGL((v10_chunked_kernel<XT, 8, LUT>), dim3(grid), dim3(kV10Threads), 0, stream, p);
+    hipLaunchKernelGGL((v10_chunked_kernel<XT, 8, LUT, LW>), dim3(grid), dim3(kV10Groups * LW), 0, stream, p);
   return hipGetLastError();
 }
 
+template <typename XT, bool LUT>
+hipError_t launch_x(const V10Params& p, int kpad, hipStream_t stream) {
+  if (p.lanes == 8) return launch_w<XT, LUT, 8>(p, kpad, stream);
+  if (p.lanes == 16) return launch_w<XT, LUT, 16>(p, kpad, stream);
+  return hipErrorInvalidValue;
+}
+
 }  // namespace
+
+int v10_lanes(int64_t B, int64_t H, int64_t hd) {
+  return B * H * ((hd + 15) / 16) >= 512 ? 16 : 8;
+}
 
 hipError_t launch_v10(const V10Params& p, int x_dtype, bool use_lut, int kpad, hipStream_t stream) {
   if (x_dtype == 0) return use_lut ? launch_x<float, true>(p, kpad, stream) : launch_x<float, false>(p, kpad, stream);

@@ -27,6 +27,7 @@ class Config:
     ttt: bool = False
     chunk: int = 0  # >0: processed as consecutive chunks with EMA carry
     bwd: bool = False  # the backward pass (dL/dx, dL/dc, dL/d ema_init) instead of the forward
+    v10: int = 0       # >0: the reference's full path (online TTT + Lion) with chunks of this many tokens
 
     @property
     def hd(self) -> int:
@@ -42,6 +43,8 @@ CONFIGS = {
     "bf16_ttt": Config("bf16_ttt", B=16, S=65536, D=512, H=8, dtype=torch.bfloat16, ttt=True),
     # the backward of configs[1]
     "backward": Config("backward", B=4, S=16384, D=512, H=8, bwd=True),
+    # the reference's full apply_cheby_rkv_v10 path at the configs[1] shape
+    "v10_full": Config("v10_full", B=4, S=16384, D=512, H=8, v10=256),
 }
 
 

@@ -50,6 +50,7 @@ def oracle(x, c, m, **kw):
     (2, 1300, 4, 16, 6, 512, True),     # chunks of two 256-token blocks
     (1, 700, 8, 16, 8, 700, True),      # S <= chunk: one chunk of 700
     (2, 257, 4, 16, 8, 256, True),      # a 1-token last chunk (NaN momentum, as the reference)
+    (8, 300, 8, 128, 8, 256, True),     # >= 512 workgroups of 16 lanes: the 16-lane kernel
 ])
 def test_v10_full_path_matches_oracle(dev, B, S, H, hd, K, chunk, use_lut):
     x, c, m = case(B, S, H, hd, K, seed=S + K, mom_scale=0.01)
