@@ -33,7 +33,14 @@
  *                      682-777) and autograd through the fast path's softsign,
  *                      Chebyshev basis, damping and tanh (1722-1739), giving
  *                      dL/dx, dL/dc and dL/d ema_init from dL/dout and
- *                      dL/d ema_final.
+ *                      dL/d ema_final.  With OSM_FLAG_FULL_JACOBIAN and
+ *                      z_saved it is the per-chunk FusedChebyRKVv10.backward
+ *                      (sdpc_kernel.py:2436-2515) of the full path.
+ *   osm_v10_chunked_ttt  the full path of apply_cheby_rkv_v10: its chunk loop
+ *                      (sdpc_kernel.py:2574-2606) of FusedChebyRKVv10.forward
+ *                      launches (2353-2433) running _ortho_megakernel
+ *                      (1890-2287) with the inline Lion update, all chunks in
+ *                      one launch.
  *
  * Conventions
  *   - All device pointers are caller-owned; the library allocates nothing.

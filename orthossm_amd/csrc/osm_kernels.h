@@ -127,8 +127,8 @@ struct BwdParams {
 // order.  Needs no workspace.  The chunks of a lane are sequential, so the
 // lanes are the only parallelism: 16 lanes per workgroup when that still
 // gives >= 512 workgroups, else 8 (v10_lanes).
-constexpr int kV10Groups = 32;    // token groups (runs) per 256-token block
-constexpr int kV10Run = 8;        // tokens per run
+constexpr int kV10Groups = 64;    // token groups (runs) per 256-token block
+constexpr int kV10Run = 4;        // tokens per run
 int v10_lanes(int64_t B, int64_t H, int64_t hd);
 struct V10Params {
   const void* x;

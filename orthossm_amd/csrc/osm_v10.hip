@@ -16,10 +16,11 @@
 // Chunks depend on each other only through (c, m) of each lane, so one
 // workgroup owns LW lanes of one (batch row, head) and walks the
 // chunks in order; the dependency never leaves the workgroup.  A chunk is
-// processed in 256-token blocks: thread (group g, lane l) owns a run of
-// kV10Run tokens; runs are composed by a scan in LDS; the proxy-gradient
-// sums are reduced over the runs in a fixed order, and LW * K threads
-// apply Lion and publish the next chunk's coefficients through LDS.
+// processed in 256-token blocks: thread (run g, lane l) owns kV10Run tokens;
+// runs are composed by a shuffle scan inside each wave and across waves in
+// LDS; the proxy-gradient sums are reduced over the runs in a fixed order,
+// and (lanes x K) threads apply Lion and publish the next chunk's
+// coefficients through LDS.
 #include "osm_tile.h"
 
 namespace osm {
@@ -50,22 +51,28 @@ __device__ __forceinline__ void v10_softsign(float xb, float& absu, float& sgn) 
 
 template <int LW>
 struct V10Lds {
+  static constexpr int NW = kV10Groups * LW / 64;   // waves per workgroup
   float lut[256][8];                 // T_k at the table's grid, k contiguous
   float cs[8][LW];                   // coefficients of the current chunk
   float ms[8][LW];                   // Lion momentum
-  float aggA[kV10Groups][LW];
-  float aggB[kV10Groups][LW];
+  float wA[NW][LW], wB[NW][LW];      // each wave's composed EMA map over its runs
   float carry[LW];                   // EMA state entering the block
-  float gc[kV10Groups][8][LW];
+  float ws[NW][8][LW];               // each wave's proxy-gradient sums
 };
 
-// LW lanes per workgroup (8 or 16), kV10Groups runs of kV10Run tokens each.
+// LW lanes per workgroup (8 or 16); kV10Groups runs of kV10Run tokens per
+// 256-token block.  A wave holds 64 / LW runs of the same LW lanes: runs are
+// composed inside a wave with shuffles and across waves through LDS, both
+// in a fixed order.
 template <typename XT, int KP, bool LUT, int LW>
 __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10Params p) {
   constexpr int kThreads = kV10Groups * LW;
+  constexpr int GPW = 64 / LW;        // runs per wave
+  constexpr int R = kV10Run;
   __shared__ V10Lds<LW> L;
   const int tid = threadIdx.x;
   const int l = tid % LW, g = tid / LW;
+  const int wave = tid >> 6, gw = (tid & 63) / LW;   // run inside the wave
   const int lg = blockIdx.x % p.n_lg;
   const int bh = blockIdx.x / p.n_lg;
   const int h = bh % p.H, b = bh / p.H;
@@ -85,6 +92,18 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
   }
   const float gamma = 0.98f - 0.06f * (float)h / (float)p.H;
   const float mu = p.mu, one_m = 1.0f - p.mu;
+  // Lion constants of this thread's (k, lane) slot, loaded once (the threads
+  // tid < KP * LW apply Lion after every chunk).
+  float lion_lr = 0.0f, lion_decay = 0.0f, lion_ss = 0.0f;
+  if (tid < KP * LW) {
+    const int k = tid / LW;
+    lion_lr = p.base_lr * p.lr_scale[h];
+    float lam = p.lion_lambda[h];
+    if (p.dyn_lambda) lam = __builtin_fminf(__builtin_fmaxf(lam + 0.008f * (p.dyn_lambda[b] - 0.5f), 0.90f), 0.9999f);
+    if (p.gate) lion_lr *= p.gate[b];
+    lion_decay = lam - lion_lr * p.wd;
+    lion_ss = k < p.K ? p.spectral_scale[k] : 0.0f;
+  }
 
   // Row descriptors over the whole sequence of this batch row.
   const Rsrc xr = make_rsrc(static_cast<const char*>(p.x) + (int64_t)b * p.x_sb * sizeof(XT),
@@ -106,22 +125,19 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
   // first token after the block), for the pair (t, t+1) of its last token.
   // Rows past S read 0; rows past the chunk are loaded but not used.
   const int n_chunks = (p.S + p.chunk - 1) / p.chunk;
-  auto run_voff = [&](int t0) -> uint32_t {
-    return lane_ok ? (uint32_t)t0 * x_row + (uint32_t)(d * sizeof(XT)) : kOffOOB;
-  };
-  float xcur[kV10Run + 1], xnxt[kV10Run + 1];
-  auto load_run = [&](float (&dst)[kV10Run + 1], int t0) {
-    const uint32_t vo_ = run_voff(t0);
+  float xcur[R + 1], xnxt[R + 1];
+  auto load_run = [&](float (&dst)[R + 1], int t0) {
+    const uint32_t vo_ = lane_ok ? (uint32_t)t0 * x_row + (uint32_t)(d * sizeof(XT)) : kOffOOB;
     uint32_t so = 0;
 #pragma unroll
-    for (int r = 0; r <= kV10Run; ++r) {
+    for (int r = 0; r <= R; ++r) {
       float t[1];
       BufVec<XT, 1>::load(xr, vo_, so, t);
       dst[r] = t[0];
       so = next_off(so, x_row);
     }
   };
-  load_run(xcur, g * kV10Run);
+  load_run(xcur, g * R);
 
   for (int ch = 0; ch < n_chunks; ++ch) {
     const int t_chunk = ch * p.chunk;
@@ -139,26 +155,26 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
     if (tid < LW) L.carry[tid] = 0.0f;
 
     for (int blk = 0; blk * kBlockTok < len; ++blk) {
-      const int r0 = blk * kBlockTok + g * kV10Run;      // run start inside the chunk
-      const int n_valid = max(0, min(kV10Run, len - r0));
+      const int r0 = blk * kBlockTok + g * R;            // run start inside the chunk
+      const int n_valid = max(0, min(R, len - r0));
       const int t0 = t_chunk + r0;                        // run start in the sequence
       // Prefetch the next block's rows.
       int t_next = -1;
       if ((blk + 1) * kBlockTok < len)
-        t_next = t_chunk + (blk + 1) * kBlockTok + g * kV10Run;
+        t_next = t_chunk + (blk + 1) * kBlockTok + g * R;
       else if (ch + 1 < n_chunks)
-        t_next = t_chunk + p.chunk + g * kV10Run;
+        t_next = t_chunk + p.chunk + g * R;
       if (t_next >= 0) load_run(xnxt, t_next);
 
-      float u[kV10Run + 1], w[kV10Run];
+      float u[R + 1], w[R];
       float A = 1.0f, Bv = 0.0f;
 #pragma unroll
-      for (int r = 0; r <= kV10Run; ++r) {
+      for (int r = 0; r <= R; ++r) {
         const float xb = to_bf16_value<XT>(xcur[r]);
         float absu, sgn;
         v10_softsign(xb, absu, sgn);
         u[r] = sgn * absu;
-        if (r == kV10Run) break;   // the row after the run: u only
+        if (r == R) break;   // the row after the run: u only
         float y;
         if constexpr (LUT) {
           const float fidx = absu * 255.0f;
@@ -205,15 +221,34 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
                                    (uint32_t)r * z_row, zz);
         }
       }
-      L.aggA[g][l] = A;
-      L.aggB[g][l] = Bv;
+      // Compose the runs: inclusive scan inside the wave (later map applied
+      // after earlier: A = A_l A_e, B = A_l B_e + B_l), then the waves.
+      float iA = A, iB = Bv;
+#pragma unroll
+      for (int o = 1; o < GPW; o <<= 1) {
+        const float pA = __shfl_up(iA, o * LW, 64), pB = __shfl_up(iB, o * LW, 64);
+        if (gw >= o) {
+          iB = __builtin_fmaf(iA, pB, iB);
+          iA *= pA;
+        }
+      }
+      float eA = __shfl_up(iA, LW, 64), eB = __shfl_up(iB, LW, 64);
+      if (gw == 0) {
+        eA = 1.0f;
+        eB = 0.0f;
+      }
+      if (gw == GPW - 1) {
+        L.wA[wave][l] = iA;
+        L.wB[wave][l] = iB;
+      }
       __syncthreads();
       float s = L.carry[l];
-      for (int q = 0; q < g; ++q) s = __builtin_fmaf(L.aggA[q][l], s, L.aggB[q][l]);
+      for (int q = 0; q < wave; ++q) s = __builtin_fmaf(L.wA[q][l], s, L.wB[q][l]);
+      s = __builtin_fmaf(eA, s, eB);
       // Replay, store bf16(s), proxy gradient.
       const uint32_t ovo = lane_ok ? (uint32_t)t0 * o_row + (uint32_t)(d * 4) : kOffOOB;
 #pragma unroll
-      for (int r = 0; r < kV10Run; ++r) {
+      for (int r = 0; r < R; ++r) {
         if (r < n_valid) {
           s = __builtin_fmaf(mu, s, w[r]);
           const float so = __builtin_amdgcn_fmed3f(s, -1.0f, 1.0f);
@@ -236,37 +271,39 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
           }
         }
       }
-      __syncthreads();   // all reads of carry and the aggregates done
+      __syncthreads();   // all reads of the carry and the wave maps done
       if (g == kV10Groups - 1) {
         // state after the block's last valid token (invalid tokens are skipped)
         L.carry[l] = s;
       }
       __syncthreads();
 #pragma unroll
-      for (int r = 0; r <= kV10Run; ++r) xcur[r] = xnxt[r];
+      for (int r = 0; r <= R; ++r) xcur[r] = xnxt[r];
     }
 
-    // Reduce the proxy gradient over the runs (fixed order), then Lion.
+    // Reduce the proxy gradient over the runs (a fixed butterfly inside each
+    // wave, then the waves in order), then Lion.
 #pragma unroll
-    for (int k = 0; k < KP; ++k) L.gc[g][k][l] = gc[k];
+    for (int k = 0; k < KP; ++k) {
+      float v = gc[k];
+#pragma unroll
+      for (int o = LW; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+      if (gw == 0) L.ws[wave][k][l] = v;
+    }
     __syncthreads();
     if (tid < KP * LW) {
       const int k = tid / LW, ll = tid % LW;
       float G = 0.0f;
-      for (int q = 0; q < kV10Groups; ++q) G += L.gc[q][k][ll];
+#pragma unroll
+      for (int q = 0; q < V10Lds<LW>::NW; ++q) G += L.ws[q][k][ll];
       if (k < p.K) {
         const float inv_s = 1.0f / (float)(len - 1);   // len = 1: inf, as the reference (NaN momentum)
         const float gk = G * inv_s;
-        float lr = p.base_lr * p.lr_scale[h];
-        float lam = p.lion_lambda[h];
-        if (p.dyn_lambda) lam = __builtin_fminf(__builtin_fmaxf(lam + 0.008f * (p.dyn_lambda[b] - 0.5f), 0.90f), 0.9999f);
-        if (p.gate) lr *= p.gate[b];
-        const float decay = lam - lr * p.wd;
         const float m = L.ms[k][ll];
         const float interp = p.beta1 * m + (1.0f - p.beta1) * gk;
         const float sg = interp > 0.0f ? 1.0f : (interp < 0.0f ? -1.0f : 0.0f);
         L.ms[k][ll] = p.beta2 * m + (1.0f - p.beta2) * gk;
-        L.cs[k][ll] = decay * L.cs[k][ll] + lr * p.spectral_scale[k] * sg;
+        L.cs[k][ll] = lion_decay * L.cs[k][ll] + lion_lr * lion_ss * sg;
       }
     }
     __syncthreads();

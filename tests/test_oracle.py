@@ -189,16 +189,20 @@ def test_chunked_with_carry_equals_monolithic(chunk):
 # ---------------------------------------------------------------- TTT gradient
 @pytest.mark.parametrize("dyn,target", [(False, "x"), (True, "x"), (False, "softsign")])
 def test_ttt_adjoint_matches_autograd(dyn, target):
+    # own generator: the module-level one's state depends on test order
+    r = np.random.default_rng(40 + 2 * dyn + (target == "x"))
     B, S, H, hd, K = 2, 33, 2, 4, 8
-    x = rng.standard_normal((B, S, H * hd))
-    c = rng.standard_normal((B, H, K, hd)) / np.arange(1, K + 1).reshape(1, 1, K, 1)
-    g = rng.uniform(-1, 1, size=(B, S, H)) if dyn else None
-    init = rng.uniform(-0.5, 0.5, size=(B, H * hd))
+    x = r.standard_normal((B, S, H * hd))
+    c = r.standard_normal((B, H, K, hd)) / np.arange(1, K + 1).reshape(1, 1, K, 1)
+    g = r.uniform(-1, 1, size=(B, S, H)) if dyn else None
+    init = r.uniform(-0.5, 0.5, size=(B, H * hd))
     kw = dict(g=g, lam_shift=0.05, ema_init=init, target=target)
     G, out, fin = O.ttt_grad(x, c, [1.0, 0.8], [0.9, 0.97], **kw)
     Ga, outa, fina = O.ttt_grad_autograd(x, c, [1.0, 0.8], [0.9, 0.97], **kw)
-    np.testing.assert_allclose(G, Ga, rtol=1e-10, atol=1e-14)
-    np.testing.assert_allclose(out, outa, rtol=1e-13)
+    # adjoint sums and autograd sums round differently: elements that cancel
+    # to near zero are compared against the gradient's scale
+    np.testing.assert_allclose(G, Ga, rtol=1e-10, atol=1e-12 * np.abs(Ga).max())
+    np.testing.assert_allclose(out, outa, rtol=1e-13, atol=1e-15 * np.abs(outa).max())
 
 
 def test_ttt_gradient_matches_central_finite_differences():
