@@ -68,7 +68,7 @@
 extern "C" {
 #endif
 
-#define OSM_ABI_VERSION 1
+#define OSM_ABI_VERSION 2
 #define OSM_MAX_K 8
 
 typedef enum osm_dtype { OSM_F32 = 0, OSM_BF16 = 1 } osm_dtype;
@@ -208,6 +208,10 @@ typedef struct osm_v10_args {
   void* z_save;                 /* optional [B,S,H*hd] bf16: z of every token (for the backward) */
   int64_t z_stride_b, z_stride_s;
   float* coeff_hist;            /* optional [ceil(S/chunk),B,H,K,hd] fp32: the coefficients each chunk used */
+  const float* ema_momentum_dev; /* optional device fp32 scalar: mu is read from it and
+                                   ema_momentum is ignored, so a mu computed on the device
+                                   (the engine's schedule, sdpc_engine.py:199-209) never
+                                   has to reach the host */
 } osm_v10_args;
 
 /* Which entry point a workspace is sized for. */

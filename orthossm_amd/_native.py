@@ -12,7 +12,7 @@ import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libosm.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 MAX_K = 8
 F32 = 0
 BF16 = 1
@@ -149,6 +149,7 @@ class V10Args(ctypes.Structure):
         ("z_stride_b", ctypes.c_int64),
         ("z_stride_s", ctypes.c_int64),
         ("coeff_hist", ctypes.c_void_p),
+        ("ema_momentum_dev", ctypes.c_void_p),
     ]
 
 

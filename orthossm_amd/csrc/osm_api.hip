@@ -342,6 +342,7 @@ int osm_v10_chunked_ttt(const osm_v10_args* a, void* stream) {
   if (a->c_stride_b < 0 || a->c_stride_h < 0 || a->c_stride_k < 0 || a->m_stride_b < 0 || a->m_stride_h < 0 ||
       a->m_stride_k < 0)
     return fail(OSM_E_LAYOUT, "coeffs/momentum strides must be non-negative");
+  if ((uintptr_t)a->ema_momentum_dev % 4) return fail(OSM_E_LAYOUT, "ema_momentum_dev misaligned");
   osm::V10Params p{};
   p.x = a->x;
   p.out = a->out;
@@ -379,6 +380,7 @@ int osm_v10_chunked_ttt(const osm_v10_args* a, void* stream) {
   p.lanes = osm::v10_lanes(a->B, a->H, a->hd);
   p.n_lg = (int)((a->hd + p.lanes - 1) / p.lanes);
   p.mu = a->ema_momentum;
+  p.mu_dev = a->ema_momentum_dev;
   p.base_lr = a->base_lr;
   p.beta1 = a->beta1;
   p.beta2 = a->beta2;

@@ -145,6 +145,7 @@ struct V10Params {
   const float* dyn_lambda;     // [B] or NULL
   void* z_save;                // bf16 [B,S,D] or NULL
   float* coeff_hist;           // [n_chunks][B,H,K,hd] or NULL
+  const float* mu_dev;         // device scalar overriding mu, or NULL
   int64_t x_sb, x_ss, o_sb, o_ss, z_sb, z_ss;
   int64_t c_sb, c_sh, c_sk, m_sb, m_sh, m_sk;
   int B, S, H, hd, K, D, chunk, n_lg;

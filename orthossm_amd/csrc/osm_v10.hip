@@ -91,7 +91,7 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
     L.ms[k][ll] = ok ? p.momentum[(int64_t)b * p.m_sb + (int64_t)h * p.m_sh + (int64_t)k * p.m_sk + jj] : 0.0f;
   }
   const float gamma = 0.98f - 0.06f * (float)h / (float)p.H;
-  const float mu = p.mu, one_m = 1.0f - p.mu;
+  const float mu = p.mu_dev ? *p.mu_dev : p.mu, one_m = 1.0f - mu;
   // Lion constants of this thread's (k, lane) slot, loaded once (the threads
   // tid < KP * LW apply Lion after every chunk).
   float lion_lr = 0.0f, lion_decay = 0.0f, lion_ss = 0.0f;

@@ -345,8 +345,28 @@ def v10_tables(device: torch.device, n_heads: int, K: int):
         return hit
 
 
+def device_momentum(mu, dev: torch.device):
+    """ema_momentum as (float, None), or, given a one-element tensor, as
+    (0.0, that value in a [1] fp32 tensor on ``dev``): a momentum computed on
+    the device stays there, with no host synchronisation."""
+    if isinstance(mu, torch.Tensor):
+        if mu.numel() != 1:
+            raise ValueError(f"ema_momentum must be a number or a one-element tensor, got shape {tuple(mu.shape)}")
+        return 0.0, mu.detach().to(device=dev, dtype=torch.float32).reshape(1).contiguous()
+    return float(mu), None
+
+
+def head_momentum(mu, n_heads: int, dev: torch.device) -> torch.Tensor:
+    """[n_heads] fp32 on ``dev``, every entry the scalar momentum ``mu`` (a
+    number or a one-element tensor, which is not read back to the host)."""
+    val, t = device_momentum(mu, dev)
+    if t is not None:
+        return t.expand(n_heads).contiguous()
+    return torch.full((n_heads,), val, dtype=torch.float32, device=dev)
+
+
 def v10_chunked_ttt(x: torch.Tensor, coeffs: torch.Tensor, momentum: torch.Tensor, *, n_heads: int,
-                    base_lr: float = 0.005, ema_momentum: float = 0.9, beta1: float = 0.9, beta2: float = 0.99,
+                    base_lr: float = 0.005, ema_momentum: float | torch.Tensor = 0.9, beta1: float = 0.9, beta2: float = 0.99,
                     weight_decay: float = 0.01, chunk_size: int = 256, gate_global: torch.Tensor | None = None,
                     dynamic_lambda: torch.Tensor | None = None, use_lut: bool = True,
                     save_for_backward: bool = False):
@@ -356,7 +376,8 @@ def v10_chunked_ttt(x: torch.Tensor, coeffs: torch.Tensor, momentum: torch.Tenso
 
     x [B,S,D] fp32|bf16, coeffs and momentum [B,H,K,hd] (cast to fp32; K > 8:
     coefficients past the eighth are returned unchanged, as the reference's
-    kernel leaves them), gate_global / dynamic_lambda optional [B].  Returns
+    kernel leaves them), gate_global / dynamic_lambda optional [B];
+    ema_momentum a number or a one-element device tensor.  Returns
     (out [B,S,D] fp32 holding bf16 values, coeffs_new, momentum_new) and, with
     save_for_backward, also (z [B,S,D] bf16, coeff_hist [n_chunks,B,H,K,hd]).
     """
@@ -413,14 +434,16 @@ def v10_chunked_ttt(x: torch.Tensor, coeffs: torch.Tensor, momentum: torch.Tenso
         lr_scale.data_ptr(), ss.data_ptr()
     a.gate = gate.data_ptr() if gate is not None else None
     a.dyn_lambda = dyn.data_ptr() if dyn is not None else None
-    a.ema_momentum, a.base_lr, a.beta1, a.beta2, a.weight_decay = (float(ema_momentum), float(base_lr),
+    mu_val, mu_dev = device_momentum(ema_momentum, dev)
+    a.ema_momentum, a.base_lr, a.beta1, a.beta2, a.weight_decay = (mu_val, float(base_lr),
                                                                    float(beta1), float(beta2), float(weight_decay))
+    a.ema_momentum_dev = mu_dev.data_ptr() if mu_dev is not None else None
     if z is not None:
         a.z_save, a.z_stride_b, a.z_stride_s = z.data_ptr(), z.stride(0), z.stride(1)
         a.coeff_hist = hist.data_ptr()
     stream = torch.cuda.current_stream(dev).cuda_stream
     nat.check(lib.osm_v10_chunked_ttt(ctypes.byref(a), ctypes.c_void_p(stream)))
-    keep = (x, c, m, gate, dyn)  # noqa: F841  (alive until the launch is queued)
+    keep = (x, c, m, gate, dyn, mu_dev)  # noqa: F841  (alive until the launch is queued)
     if Kfull > K:
         c_out = torch.cat([c_out, c_full[:, :, K:]], dim=2)
         m_out = torch.cat([m_out, m_full[:, :, K:]], dim=2)
@@ -441,7 +464,7 @@ def _v10_backward(x, out, z, hist, grad_out, n_heads, ema_momentum, chunk, need_
     dev = x.device
     h = torch.arange(H, dtype=torch.float32, device=dev)
     damping = (0.98 - 0.06 * h / H).contiguous()
-    lam = torch.full((H,), float(ema_momentum), dtype=torch.float32, device=dev)
+    lam = head_momentum(ema_momentum, H, dev)
     go = grad_out.to(dtype=torch.float32).contiguous()
     xc = x.contiguous()
     gx = torch.empty_like(xc)

@@ -28,7 +28,7 @@ from __future__ import annotations
 
 import torch
 
-from .ops import cheby_ema, cheby_ema_forward, v10_chunked_ttt, v10_full_path
+from .ops import cheby_ema, cheby_ema_forward, head_momentum, v10_chunked_ttt, v10_full_path
 
 
 def v10_damping(n_heads: int, device=None) -> torch.Tensor:
@@ -42,7 +42,10 @@ def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_m
                         gate_global=None, dynamic_lambda=None, use_lut=True, seq_threshold=384,
                         lion_max_norm=14.0):
     """Same signature and return convention as the reference:
-    returns (out [B,S,D] fp32, coeffs fp32, momentum_buf fp32 or None)."""
+    returns (out [B,S,D] fp32, coeffs fp32, momentum_buf fp32 or None).
+    ``ema_momentum`` may also be a one-element tensor on the device, read
+    there by the kernels (the reference takes a Python float, which its
+    engine obtains with a host synchronisation, sdpc_engine.py:209)."""
     B, S, D = x.shape
     if coeffs.dtype != torch.float32:
         coeffs = coeffs.float()
@@ -61,7 +64,7 @@ def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_m
             dynamic_lambda=dynamic_lambda, use_lut=use_lut)
         return out, c_new, m_new
     damping = v10_damping(H, x.device)
-    lam = torch.full((H,), float(ema_momentum), dtype=torch.float32, device=x.device)
+    lam = head_momentum(ema_momentum, H, x.device)
     if torch.is_grad_enabled() and (x.requires_grad or coeffs.requires_grad):
         out = cheby_ema(x, coeffs, damping, lam, out_dtype=torch.float32, nan_policy="zero_u")
     else:

@@ -186,6 +186,7 @@ def _v10(**kw):
     (dict(momentum=0), -1),
     (dict(out_stride_s=32), -4),       # rows overlap
     (dict(x_stride_s=1 << 22), -4),    # a batch row over 2 GiB
+    (dict(ema_momentum_dev=0x10002), -4),   # device momentum not float-aligned
 ])
 def test_v10_argument_errors(kw, code):
     lib = nat.load()
