@@ -151,6 +151,11 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
   __shared__ float mono[KP][kLanes];
   __shared__ float sh_red[G::WAVES][KP][kLanes];
 
+  // Highest wave priority while the tile's loads are issued (here and
+  // before the x loads below), so that they enter the memory pipeline ahead
+  // of other workgroups' arithmetic (measured at BASELINE configs[1] on
+  // MI355X: 121.8 against 124.0 us).
+  __builtin_amdgcn_s_setprio(3);
   const ThreadPos q = thread_pos<G>();
   ThreadPos qc = q;
   qc.tg = G::NTG - 1 - q.tg;   // chain order: the tile's last run first
@@ -206,6 +211,7 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
       sg = next_off(sg, a.sg);
     }
   }
+  __builtin_amdgcn_s_setprio(0);
   mono_store<KP, G>(ml, q, mono);   // read after the chain's barriers
 
   // Pass 1: the run's map v[t0] = A v[t_end + 1] + B, last token first.
@@ -246,6 +252,7 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
 
   // x loads (kept in order after pass 1 by the barrier).
   asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_setprio(3);
   {
     uint32_t so = 0;
 #pragma unroll
@@ -269,6 +276,7 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
     }
   }
 
+  __builtin_amdgcn_s_setprio(0);
   const LaneSlots ls = lane_slots<G, true>(p.slots, ti, p.n_tiles);
   float pA, pB[1], aggA, aggB;
   tile_scan<G, true>(L, qc, ti, tags, A, Bv, pA, pB, aggA, aggB, ls);

@@ -89,6 +89,11 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   constexpr int LPT = G::LPT;
   __shared__ ChainLds<G> L;
 
+  // Highest wave priority until the tile's loads are issued: a workgroup
+  // that has just started gets its loads into the memory pipeline ahead of
+  // the arithmetic of older workgroups on the CU (measured at BASELINE
+  // configs[1] on MI355X: 52.0 against 53.5 us).
+  __builtin_amdgcn_s_setprio(3);
   const ThreadPos q = thread_pos<G>();
   const Tags tags = launch_tags(p.hdr);
   const TileInfo ti = tile_info<G>(blockIdx.x, p.n_lb, p.n_lb_pad, p.n_lbd, p.n_tiles);
@@ -125,6 +130,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     }
   }
 
+  __builtin_amdgcn_s_setprio(0);
   mono_store<KP, G>(ml, q, mono);
   __syncthreads();
   float c[LPT][KP];
