@@ -138,6 +138,12 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
     }
   };
   load_run(xcur, g * R);
+  // Wait for these rows here, once.  Without it the compiler, merging this
+  // path with the loop's back edge, waits for the next block's prefetched
+  // rows at the start of every block (vmcnt 4..1 before each row's use),
+  // which exposes a full memory latency per chunk (283 against 299 us at
+  // the configs[1] shape).  s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15).
+  __builtin_amdgcn_s_waitcnt(0xF70);
 
   for (int ch = 0; ch < n_chunks; ++ch) {
     const int t_chunk = ch * p.chunk;
@@ -271,12 +277,16 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
           }
         }
       }
-      __syncthreads();   // all reads of the carry and the wave maps done
-      if (g == kV10Groups - 1) {
-        // state after the block's last valid token (invalid tokens are skipped)
-        L.carry[l] = s;
+      if (len > kBlockTok) {
+        // The next block of this chunk starts from this block's end state
+        // (a one-block chunk has no next block: the carry restarts at 0).
+        __syncthreads();   // all reads of the carry and the wave maps done
+        if (g == kV10Groups - 1) {
+          // state after the block's last valid token (invalid tokens are skipped)
+          L.carry[l] = s;
+        }
+        __syncthreads();
       }
-      __syncthreads();
 #pragma unroll
       for (int r = 0; r <= R; ++r) xcur[r] = xnxt[r];
     }
