@@ -89,9 +89,13 @@ __device__ __forceinline__ MonoLoad<KP, G> mono_issue(const FwdParams& p, const 
     const uint32_t vc = ok ? (uint32_t)(((int64_t)h * p.c_sh + (d - h * p.hd)) * 4) : kOffOOB;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      // Unconditional loads (an unused unit or k >= K reads 0 through the
+      // out-of-range offset): a branch here would make the compiler convert
+      // each value inside it and so wait for every load on the spot, before
+      // the caller's bulk loads are issued.
       const int k = j + 2 * i;
-      float v[1] = {0.0f};
-      if (u < m.NU) BufVec<float, 1>::load(a.c, k < p.K ? vc : kOffOOB, (uint32_t)k * a.sc, v);
+      float v[1];
+      BufVec<float, 1>::load(a.c, k < p.K ? vc : kOffOOB, (uint32_t)k * a.sc, v);
       m.cm[n][i] = v[0];
     }
     m.kap[n] = kTwoLog2e * p.damping[h];
