@@ -254,15 +254,33 @@ __device__ __forceinline__ void look_back_finish(LookBack<G, DYN>& st, ChainLds<
   __syncthreads();
 }
 
-// Counts this block as finished.  The last block of its class resets the
-// class counter; the last class bumps the epoch for the next launch.
-__device__ __forceinline__ void finish_block(unsigned* hdr_words, unsigned epoch) {
+// Counting the blocks of a launch, in two halves: finish_issue counts this
+// block (thread 0), finish_complete acts on the count.  The last block of its
+// class resets the class counter; the last class bumps the epoch for the next
+// launch.  Safe once this block's epoch read (launch_tags) has returned,
+// which the increment's data dependency on the epoch enforces: blocks of
+// this launch use the epoch they read at their start, so a bump while some
+// of them still publish or wait changes nothing for them.  Split so that the
+// counter's round trip overlaps the block's work and its result is read
+// before the block's bulk stores (loads and stores share one wait counter, so
+// reading it after them would wait for every store).
+__device__ __forceinline__ unsigned finish_issue(unsigned* hdr_words, unsigned epoch) {
+  unsigned prev = 0;
+  if (threadIdx.x == 0) {
+    WsHeader* hdr = reinterpret_cast<WsHeader*>(hdr_words);
+    unsigned one = 1u;
+    asm volatile("" : "+v"(one) : "v"(epoch));   // the count depends on the epoch value
+    prev = __hip_atomic_fetch_add(&hdr->cls[blockIdx.x & 7u].done, one, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return prev;
+}
+
+__device__ __forceinline__ void finish_complete(unsigned* hdr_words, unsigned epoch, unsigned prev) {
   if (threadIdx.x == 0) {
     WsHeader* hdr = reinterpret_cast<WsHeader*>(hdr_words);
     const unsigned cls = blockIdx.x & 7u;
     const unsigned cls_size = (gridDim.x - cls + 7u) >> 3;
-    const unsigned prev = __hip_atomic_fetch_add(&hdr->cls[cls].done, 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
     if (prev == cls_size - 1u) {
       __hip_atomic_store(&hdr->cls[cls].done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const unsigned n_cls = gridDim.x < 8u ? gridDim.x : 8u;
@@ -274,6 +292,11 @@ __device__ __forceinline__ void finish_block(unsigned* hdr_words, unsigned epoch
       }
     }
   }
+}
+
+// Both halves at once (blocks without a tile, and the end of a kernel).
+__device__ __forceinline__ void finish_block(unsigned* hdr_words, unsigned epoch) {
+  finish_complete(hdr_words, epoch, finish_issue(hdr_words, epoch));
 }
 
 }  // namespace osm

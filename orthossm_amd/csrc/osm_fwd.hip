@@ -191,6 +191,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
 #pragma unroll
   for (int i = 0; i < LPT; ++i) bad |= Bv[i] != Bv[i];
   if (bad) pass1_exact<G, DYN, XT, KP>(w, a, c, lamv, Bv, p.nan_zero_u != 0);
+  const unsigned fin_prev = finish_issue(p.hdr, tags.epoch);
 
   const LaneSlots ls = lane_slots<G, DYN>(p.slots, ti, p.n_tiles);
   float pA, pB[LPT], aggA, aggB;
@@ -204,6 +205,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     look_back_issue<G, DYN>(lbk, q, ti, ls);
     look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, lam_look, p.hdr);
   }
+  finish_complete(p.hdr, tags.epoch, fin_prev);
 
   // Pass 2: replay the recurrence from the true carry and store out.
   float s[LPT];
@@ -222,7 +224,6 @@ cheby_ema_fwd_kernel(const FwdParams p) {
                      : nullptr;
     pass2<G, OT, true>(s, w, lamv, a, lo, hi, r_last, fin);
   }
-  finish_block(p.hdr, tags.epoch);
 }
 
 template <class G, bool DYN, typename XT, typename OT>
