@@ -63,6 +63,10 @@ def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_m
             beta2=lion_beta2, weight_decay=lion_wd, chunk_size=chunk_size, gate_global=gate_global,
             dynamic_lambda=dynamic_lambda, use_lut=use_lut)
         return out, c_new, m_new
+    if coeffs.shape[2] > 8:
+        # The reference's PyTorch fast path evaluates any number of terms; its
+        # kernels (and its engine, max_degree <= 8) stop at eight.
+        raise ValueError(f"the fast path supports at most 8 Chebyshev coefficients, got {coeffs.shape[2]}")
     damping = v10_damping(H, x.device)
     lam = head_momentum(ema_momentum, H, x.device)
     if torch.is_grad_enabled() and (x.requires_grad or coeffs.requires_grad):

@@ -39,3 +39,11 @@ def test_cpu_tensor_raises():
     c = torch.zeros(1, 4, 4, 16)
     with pytest.raises(RuntimeError, match="ROCm GPU only"):
         apply_cheby_rkv_v10(x, c, None, n_heads=4)
+
+
+def test_fast_path_rejects_more_than_eight_coefficients():
+    # the reference's kernels clamp the degree to 8 (sdpc_kernel.py:2379)
+    x = torch.randn(1, 16, 32)
+    c = torch.randn(1, 4, 10, 8)
+    with pytest.raises(ValueError, match="at most 8"):
+        apply_cheby_rkv_v10(x, c, torch.zeros_like(c), n_heads=4, seq_threshold=384)
