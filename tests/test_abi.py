@@ -204,3 +204,23 @@ def test_error_messages_are_thread_local():
     t.start()
     t.join()
     assert seen == [b""] and b"K=9" in lib.osm_last_error()
+
+
+def _doc_struct(name):
+    """The ctypes mirror `name` as written in INTEGRATION.md's stubs."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    m = re.search(rf"^class {name}\(ctypes\.Structure\):.*?\]\n", text, flags=re.S | re.M)
+    assert m, f"{name} not found in INTEGRATION.md"
+    ns = {"ctypes": ctypes}
+    exec(m.group(0), ns)
+    return ns[name]
+
+
+@pytest.mark.parametrize("doc_name,cls", [("_Args", nat.ChebyArgs), ("_BwdArgs", nat.BwdArgs)])
+def test_integration_stub_structs_match_the_header(doc_name, cls):
+    # the stubs a maintainer would paste must lay the structs out as osm.h does
+    doc = _doc_struct(doc_name)
+    assert ctypes.sizeof(doc) == ctypes.sizeof(cls)
+    assert [f for f, _ in doc._fields_] == [f for f, _ in cls._fields_]
+    for f, _ in cls._fields_:
+        assert getattr(doc, f).offset == getattr(cls, f).offset, f
