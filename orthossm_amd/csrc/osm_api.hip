@@ -334,11 +334,14 @@ int osm_v10_chunked_ttt(const osm_v10_args* a, void* stream) {
     return fail(OSM_E_LAYOUT, "out rows/batches overlap");
   if (a->z_save && (a->z_stride_s < D || a->z_stride_b < a->S * a->z_stride_s || (uintptr_t)a->z_save % 2))
     return fail(OSM_E_LAYOUT, "z_save rows/batches overlap or z_save misaligned");
-  // Each batch row is addressed through one buffer descriptor (31-bit byte offsets).
+  // Rows are addressed through buffer descriptors rebased at every block of
+  // kV10Groups * kV10Run tokens: a block and the row after it must fit their
+  // 31-bit byte offsets.
   const int64_t lim = int64_t(1) << 31;
-  if (((a->S - 1) * a->x_stride_s + D) * xs >= lim || ((a->S - 1) * a->out_stride_s + D) * 4 >= lim ||
-      (a->z_save && ((a->S - 1) * a->z_stride_s + D) * 2 >= lim))
-    return fail(OSM_E_LAYOUT, "a batch row spans more than 2 GiB");
+  const int64_t blk_rows = osm::kV10Groups * osm::kV10Run + 1;
+  if ((blk_rows * a->x_stride_s + D) * xs >= lim || (blk_rows * a->out_stride_s + D) * 4 >= lim ||
+      (a->z_save && (blk_rows * a->z_stride_s + D) * 2 >= lim))
+    return fail(OSM_E_LAYOUT, "token stride too large: 257 rows span more than 2 GiB");
   if (a->c_stride_b < 0 || a->c_stride_h < 0 || a->c_stride_k < 0 || a->m_stride_b < 0 || a->m_stride_h < 0 ||
       a->m_stride_k < 0)
     return fail(OSM_E_LAYOUT, "coeffs/momentum strides must be non-negative");

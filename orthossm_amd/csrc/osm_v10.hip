@@ -105,15 +105,17 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
     lion_ss = k < p.K ? p.spectral_scale[k] : 0.0f;
   }
 
-  // Row descriptors over the whole sequence of this batch row.
-  const Rsrc xr = make_rsrc(static_cast<const char*>(p.x) + (int64_t)b * p.x_sb * sizeof(XT),
-                            ((uint64_t)(p.S - 1) * p.x_ss + p.D) * sizeof(XT));
-  const Rsrc orr = make_rsrc(reinterpret_cast<const char*>(p.out) + (int64_t)b * p.o_sb * 4,
-                             ((uint64_t)(p.S - 1) * p.o_ss + p.D) * 4);
-  Rsrc zr = orr;
-  if (p.z_save)
-    zr = make_rsrc(static_cast<const char*>(p.z_save) + (int64_t)b * p.z_sb * 2,
-                   ((uint64_t)(p.S - 1) * p.z_ss + p.D) * 2);
+  // This batch row of x, out and z.  Descriptors are rebased at each block
+  // (uniform row t_blk) and end after row S-1, so a batch row may exceed the
+  // 31-bit reach of one descriptor; a thread's offsets stay inside its block
+  // (the host checks that 257 rows fit).  Rows past S read 0, stores past S
+  // are dropped.
+  const char* const xb0 = static_cast<const char*>(p.x) + (int64_t)b * p.x_sb * (int64_t)sizeof(XT);
+  const char* const ob0 = reinterpret_cast<const char*>(p.out) + (int64_t)b * p.o_sb * 4;
+  const char* const zb0 = p.z_save ? static_cast<const char*>(p.z_save) + (int64_t)b * p.z_sb * 2 : ob0;
+  auto rows_from = [&](const char* base, int64_t stride, int64_t elem, int t_blk) {
+    return make_rsrc(base + (int64_t)t_blk * stride * elem, ((uint64_t)(p.S - 1 - t_blk) * stride + p.D) * elem);
+  };
   const uint32_t x_row = (uint32_t)(p.x_ss * sizeof(XT));   // bytes per token
   const uint32_t o_row = (uint32_t)(p.o_ss * 4);
   const uint32_t z_row = (uint32_t)(p.z_ss * 2);
@@ -126,8 +128,10 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
   // Rows past S read 0; rows past the chunk are loaded but not used.
   const int n_chunks = (p.S + p.chunk - 1) / p.chunk;
   float xcur[R + 1], xnxt[R + 1];
-  auto load_run = [&](float (&dst)[R + 1], int t0) {
-    const uint32_t vo_ = lane_ok ? (uint32_t)t0 * x_row + (uint32_t)(d * sizeof(XT)) : kOffOOB;
+  // Rows of this thread's run in the block starting at row t_blk.
+  auto load_run = [&](float (&dst)[R + 1], int t_blk) {
+    const Rsrc xr = rows_from(xb0, p.x_ss, (int64_t)sizeof(XT), t_blk);
+    const uint32_t vo_ = lane_ok ? (uint32_t)(g * R) * x_row + (uint32_t)(d * sizeof(XT)) : kOffOOB;
     uint32_t so = 0;
 #pragma unroll
     for (int r = 0; r <= R; ++r) {
@@ -137,7 +141,7 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
       so = next_off(so, x_row);
     }
   };
-  load_run(xcur, g * R);
+  load_run(xcur, 0);
   // Wait for these rows here, once.  Without it the compiler, merging this
   // path with the loop's back edge, waits for the next block's prefetched
   // rows at the start of every block (vmcnt 4..1 before each row's use),
@@ -163,14 +167,16 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
     for (int blk = 0; blk * kBlockTok < len; ++blk) {
       const int r0 = blk * kBlockTok + g * R;            // run start inside the chunk
       const int n_valid = max(0, min(R, len - r0));
-      const int t0 = t_chunk + r0;                        // run start in the sequence
+      const int t_blk = t_chunk + blk * kBlockTok;         // block start in the sequence
       // Prefetch the next block's rows.
       int t_next = -1;
       if ((blk + 1) * kBlockTok < len)
-        t_next = t_chunk + (blk + 1) * kBlockTok + g * R;
+        t_next = t_chunk + (blk + 1) * kBlockTok;
       else if (ch + 1 < n_chunks)
-        t_next = t_chunk + p.chunk + g * R;
+        t_next = t_chunk + p.chunk;
       if (t_next >= 0) load_run(xnxt, t_next);
+      const Rsrc orr = rows_from(ob0, p.o_ss, 4, t_blk);
+      const Rsrc zr = rows_from(zb0, p.z_save ? p.z_ss : p.o_ss, p.z_save ? 2 : 4, t_blk);
 
       float u[R + 1], w[R];
       float A = 1.0f, Bv = 0.0f;
@@ -223,7 +229,7 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
         }
         if (p.z_save && r < n_valid) {
           const float zz[1] = {z};
-          BufVec<__bf16, 1>::store(zr, lane_ok ? (uint32_t)t0 * z_row + (uint32_t)(d * 2) : kOffOOB,
+          BufVec<__bf16, 1>::store(zr, lane_ok ? (uint32_t)(g * R) * z_row + (uint32_t)(d * 2) : kOffOOB,
                                    (uint32_t)r * z_row, zz);
         }
       }
@@ -252,7 +258,7 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
       for (int q = 0; q < wave; ++q) s = __builtin_fmaf(L.wA[q][l], s, L.wB[q][l]);
       s = __builtin_fmaf(eA, s, eB);
       // Replay, store bf16(s), proxy gradient.
-      const uint32_t ovo = lane_ok ? (uint32_t)t0 * o_row + (uint32_t)(d * 4) : kOffOOB;
+      const uint32_t ovo = lane_ok ? (uint32_t)(g * R) * o_row + (uint32_t)(d * 4) : kOffOOB;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         if (r < n_valid) {

@@ -185,7 +185,7 @@ def _v10(**kw):
     (dict(lut=0), -1),                 # LUT mode needs the table
     (dict(momentum=0), -1),
     (dict(out_stride_s=32), -4),       # rows overlap
-    (dict(x_stride_s=1 << 22), -4),    # a batch row over 2 GiB
+    (dict(x_stride_s=1 << 22), -4),    # 257 rows over 2 GiB
     (dict(ema_momentum_dev=0x10002), -4),   # device momentum not float-aligned
 ])
 def test_v10_argument_errors(kw, code):

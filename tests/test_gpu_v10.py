@@ -179,3 +179,21 @@ def test_v10_single_chunk_grads_and_nan(dev):
     assert torch.isnan(gx[0, 5, 2])
     _close(gx, wx, "grad_x")
     _close(gc, wc, "grad_coeffs")
+
+
+def test_v10_batch_row_beyond_2gib(dev):
+    # a strided view whose batch row spans more than 2 GiB (the kernel rebases
+    # its row descriptors at every block): same bits as the contiguous input
+    S, Dbig, H, hd = 65600, 8192, 4, 16
+    x_big = torch.zeros(1, S, Dbig, device=dev)
+    x_big[:, :, :H * hd] = torch.randn(1, S, H * hd, generator=torch.Generator().manual_seed(41)).to(dev)
+    x = x_big[:, :, :H * hd]
+    assert ((S - 1) * x.stride(1) + H * hd) * 4 > 2 ** 31
+    c = (torch.randn(1, H, 8, hd, generator=torch.Generator().manual_seed(42)) * 0.3).to(dev)
+    m = torch.zeros_like(c)
+    a = v10_chunked_ttt(x, c, m, n_heads=H)
+    b = v10_chunked_ttt(x.contiguous(), c, m, n_heads=H)
+    torch.cuda.synchronize()
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    del x_big
