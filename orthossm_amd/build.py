@@ -64,7 +64,25 @@ def build(verbose: bool = False) -> str:
             os.remove(tmp)
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-8000:]}")
     os.replace(tmp, LIB_PATH)
+    build_c_smoke(verbose)
     return LIB_PATH
+
+
+C_SMOKE_SRC = os.path.join(ROOT, "tests", "c_abi", "osm_c_smoke.cpp")
+C_SMOKE_BIN = os.path.join(ROOT, "tests", "c_abi", "osm_c_smoke")
+
+
+def build_c_smoke(verbose: bool = False) -> str:
+    """Compiles the C-ABI test program (host code only, linked against the
+    library with an rpath to it), used by tests/test_gpu_c_abi.py."""
+    cmd = [hipcc_path(), *common_flags(), "-o", C_SMOKE_BIN, C_SMOKE_SRC, "-L", LIB_DIR, "-losm",
+           "-Wl,-rpath,$ORIGIN/../../orthossm_amd/_lib"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on the C-ABI test program ({res.returncode}):\n{res.stderr[-4000:]}")
+    return C_SMOKE_BIN
 
 
 if __name__ == "__main__":
