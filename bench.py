@@ -273,6 +273,21 @@ def main():
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     per = sorted(a.elapsed_time(b) for a, b in ev)
+    # Achievable copy bandwidth on this box, for reference: plain device
+    # copies of one x buffer into an output buffer (the same bytes read and
+    # written as the forward at this shape), rotating over the buffer sets.
+    n_copy = 20
+    for i in range(3):
+        outs[i % args.sets].copy_(xs[(i + 1) % args.sets])
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    c0.record(stream)
+    for i in range(n_copy):
+        outs[i % args.sets].copy_(xs[(i + 1) % args.sets])
+    c1.record(stream)
+    torch.cuda.synchronize()
+    copy_ms = c0.elapsed_time(c1) / n_copy
+    copy_gbs = 2 * xs[0].numel() * xs[0].element_size() / (copy_ms * 1e-3) / 1e9
     tokens = cfg.B * cfg.S
     algo = algorithmic_bytes(cfg)
     launches = cfg.S // cfg.chunk if cfg.chunk else 1
@@ -318,6 +333,8 @@ def main():
             "step_ms_evented_p10": per[len(per) // 10],
             "step_ms_evented_median": per[len(per) // 2],
             "step_ms_evented_p90": per[(9 * len(per)) // 10],
+            "copy_gbs_measured": copy_gbs,
+            "frac_of_copy": achieved_gbs / copy_gbs,
         },
     }
     if args.calibrate_copy:
