@@ -193,7 +193,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; the hot path shards over batch/heads with no "
-              "communication (see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "communication (batch rows and heads are independent). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)

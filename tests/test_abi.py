@@ -207,7 +207,7 @@ def test_error_messages_are_thread_local():
 
 
 def _doc_struct(name):
-    """The ctypes mirror `name` as written in INTEGRATION.md's stubs."""
+    """The ctypes structure `name` from the binding stubs of the integration guide."""
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     m = re.search(rf"^class {name}\(ctypes\.Structure\):.*?\]\n", text, flags=re.S | re.M)
     assert m, f"{name} not found in INTEGRATION.md"
