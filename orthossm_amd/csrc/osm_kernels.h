@@ -44,9 +44,14 @@ struct TileGeo {
 // tile.  Measured on MI355X at BASELINE configs[1] against 128-lane tiles
 // with 2 or 4 lanes per thread (256 and 128 tokens) and 64-lane tiles with 4
 // lanes per thread: the 64-lane, 2-lane, 512-token tile is fastest.
-using FwdTileLarge = TileGeo<2, 8, 32>;    // 512 tokens x 64 lanes
-using FwdTileMedium = TileGeo<2, 8, 16>;   // 256 tokens x 64 lanes
-using FwdTileSmall = TileGeo<2, 8, 8>;     // 128 tokens x 64 lanes
+// The medium and small tiles (dynamic lambda, and short sequences) read two
+// look-back words per thread (checkpoints every 16 tiles): every thread runs
+// the polling code of each of its words, and at configs[3] two words give
+// 427 against 449 us with eight.  The large tile keeps eight (no difference
+// at configs[1]).
+using FwdTileLarge = TileGeo<2, 8, 32>;           // 512 tokens x 64 lanes
+using FwdTileMedium = TileGeo<2, 8, 16, 64, 2>;   // 256 tokens x 64 lanes
+using FwdTileSmall = TileGeo<2, 8, 8, 64, 2>;     // 128 tokens x 64 lanes
 constexpr int kMaxTileRows = 512;              // bound on TILE (+1 row read past a tile)
 
 // Geometry of a forward launch.
@@ -60,19 +65,24 @@ FwdShape fwd_geometry(bool dyn, int64_t B, int64_t D, int64_t S);
 // run in registers, plus 2K gradient accumulators per lane: one lane per
 // thread (half the accumulators of two), 16-token runs.  Chosen by
 // measurement on MI355X at BASELINE configs[4] against 2 lanes x 8 or 16
-// tokens and 1 lane x 32 tokens (which spills).
-using TttTile = TileGeo<1, 8, 16>;   // 128 tokens
+// tokens and 1 lane x 32 tokens (which spills).  Two look-back words per
+// thread (checkpoints every 16 tiles): the kernel is VALU-bound, and every
+// thread runs the polling code of each of its words, so fewer words per
+// thread cost fewer instructions per element (1147 against 1254 us with
+// eight words and 1177 with four, at configs[4]; one word 1145).
+using TttTile = TileGeo<1, 8, 16, 64, 2>;   // 128 tokens
 int ttt_tile_tokens(bool dyn, int x_dtype);
 
 // Backward: one lane per thread (the clamp mask makes the adjoint map's A
 // differ per lane); x and dL/dout of the run stay in registers between the
 // passes (plus lambda per token with a dynamic lambda), and the look-back
 // reads two words (A, B) per predecessor.  Four look-back words per thread
-// (checkpoints every 32 tiles) instead of eight bring the static kernel from
+// (checkpoints every 32 tiles) instead of eight brought the static kernel from
 // 101 to 77 VGPRs, three workgroups per CU instead of two: 129 against 141 us
-// at BASELINE configs[1] on MI355X.  32-token runs spill; 8-token runs are
+// at BASELINE configs[1] on MI355X; two words (checkpoints every 16 tiles)
+// 116.9 against 118.2 us with four.  32-token runs spill; 8-token runs are
 // slower (185 us).
-using BwdTile = TileGeo<1, 8, 16, 64, 4>;   // 128 tokens
+using BwdTile = TileGeo<1, 8, 16, 64, 2>;   // 128 tokens
 int bwd_tile_tokens(bool dyn);
 
 // Workspace: a kHeaderBytes header (launch epoch, fault word, completion
