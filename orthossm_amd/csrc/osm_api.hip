@@ -143,6 +143,7 @@ osm::FwdParams make_params(const osm_cheby_args* a, const Geometry& geo, void* w
   p.S = (int)a->S;
   p.H = (int)a->H;
   p.hd = (int)a->hd;
+  osm::div_magic((uint32_t)a->hd, &p.hd_magic, &p.hd_shift);
   p.K = (int)a->K;
   p.D = (int)(a->H * a->hd);
   p.n_lbd = geo.n_lbd;

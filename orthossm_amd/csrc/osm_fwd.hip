@@ -200,7 +200,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     const int dc = ti.lbd * G::LANES + carry_lane<G>(q);
     const float init_c = (p.ema_init && q.wave < G::NSUB && dc < p.D) ? p.ema_init[(int64_t)ti.b * p.D + dc] : 0.0f;
     const int dlk = ti.lbd * G::LANES + look_lane<G>(q);
-    const float lam_look = DYN ? 0.0f : p.lam[dlk < p.D ? dlk / p.hd : 0];
+    const float lam_look = DYN ? 0.0f : p.lam[dlk < p.D ? div_hd(dlk, p) : 0];
     LookBack<G, DYN> lbk;
     look_back_issue<G, DYN>(lbk, q, ti, ls);
     look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, lam_look, p.hdr);

@@ -106,6 +106,8 @@ struct FwdParams {
   int64_t c_sb, c_sh, c_sk;
   int64_t g_sb, g_ss, g_sh;
   int B, S, H, hd, K, D;
+  uint32_t hd_magic;           // n / hd = (umulhi(n, hd_magic) + n) >> hd_shift for 0 <= n < 2^31
+  int hd_shift;
   int n_lbd;                   // lane-blocks per batch row = ceil(D / LANES)
   int n_lb;                    // B * n_lbd
   int n_lb_pad;                // n_lb rounded up to a multiple of 8; grid = n_lb_pad * n_tiles
@@ -162,6 +164,17 @@ struct V10Params {
   int lanes;                   // lanes per workgroup (8 or 16)
   float mu, base_lr, beta1, beta2, wd;
 };
+
+// Multiplier and shift that divide by v (1 <= v < 2^31) for dividends
+// 0 <= n < 2^31: s = ceil(log2 v), m = floor(2^32 (2^s - v) / v) + 1
+// (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", 1994, the round-up variant).
+inline void div_magic(uint32_t v, uint32_t* magic, int* shift) {
+  int s = 0;
+  while ((uint64_t(1) << s) < v) ++s;
+  *shift = s;
+  *magic = (uint32_t)((((uint64_t(1) << s) - v) << 32) / v + 1);
+}
 
 // Workspace layout helpers (bytes).
 size_t slot_words(bool dyn);

@@ -18,6 +18,11 @@ struct TileAddr {
 // x, out (and g) descriptors start at the tile's first row and end after row
 // S-1: rows past the sequence read 0 and their stores are dropped, and rows
 // after the tile (still < S) can be read through the same descriptor.
+// n / hd for 0 <= n < 2^31 (the multiplier and shift come from the host).
+__device__ __forceinline__ int div_hd(int n, const FwdParams& p) {
+  return (int)((__umulhi((uint32_t)n, p.hd_magic) + (uint32_t)n) >> p.hd_shift);
+}
+
 template <class G, bool DYN, typename XT, typename OT>
 __device__ __forceinline__ TileAddr tile_addr(const FwdParams& p, const ThreadPos& q, const TileInfo& ti) {
   TileAddr a;
@@ -25,7 +30,7 @@ __device__ __forceinline__ TileAddr tile_addr(const FwdParams& p, const ThreadPo
   const int d0 = ti.lbd * G::LANES + q.lt * G::LPT;
   const bool lane_ok = d0 < p.D;
   const uint64_t rows_after = (uint64_t)(p.S - 1 - t_tile);
-  a.h = lane_ok ? d0 / p.hd : 0;
+  a.h = lane_ok ? div_hd(d0, p) : 0;
   const int64_t row0 = (int64_t)q.tg * G::R;
   const char* xb = static_cast<const char*>(p.x) + ((int64_t)ti.b * p.x_sb + (int64_t)t_tile * p.x_ss) * sizeof(XT);
   a.x = make_rsrc(xb, (rows_after * p.x_ss + p.D) * sizeof(XT));
@@ -85,7 +90,7 @@ __device__ __forceinline__ MonoLoad<KP, G> mono_issue(const FwdParams& p, const 
     const int j = u / G::NSUB;
     const int d = ti.lbd * G::LANES + (u % G::NSUB) * kLanes + q.wl;
     const bool ok = u < m.NU && d < p.D;
-    const int h = ok ? d / p.hd : 0;
+    const int h = ok ? div_hd(d, p) : 0;
     const uint32_t vc = ok ? (uint32_t)(((int64_t)h * p.c_sh + (d - h * p.hd)) * 4) : kOffOOB;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
