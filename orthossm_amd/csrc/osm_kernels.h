@@ -44,14 +44,14 @@ struct TileGeo {
 // tile.  Measured on MI355X at BASELINE configs[1] against 128-lane tiles
 // with 2 or 4 lanes per thread (256 and 128 tokens) and 64-lane tiles with 4
 // lanes per thread: the 64-lane, 2-lane, 512-token tile is fastest.
-// The medium and small tiles (dynamic lambda, and short sequences) read two
-// look-back words per thread (checkpoints every 16 tiles): every thread runs
-// the polling code of each of its words, and at configs[3] two words give
-// 427 against 449 us with eight.  The large tile keeps eight (no difference
-// at configs[1]).
+// The medium and small tiles (dynamic lambda, and short sequences) read one
+// look-back word per thread (checkpoints every 8 tiles): every thread runs
+// the polling code of each of its words, and at configs[3] one word gives
+// 420 us against 429 with two and 449 with eight.  The large tile keeps
+// eight (no difference at configs[1]).
 using FwdTileLarge = TileGeo<2, 8, 32>;           // 512 tokens x 64 lanes
-using FwdTileMedium = TileGeo<2, 8, 16, 64, 2>;   // 256 tokens x 64 lanes
-using FwdTileSmall = TileGeo<2, 8, 8, 64, 2>;     // 128 tokens x 64 lanes
+using FwdTileMedium = TileGeo<2, 8, 16, 64, 1>;   // 256 tokens x 64 lanes
+using FwdTileSmall = TileGeo<2, 8, 8, 64, 1>;     // 128 tokens x 64 lanes
 constexpr int kMaxTileRows = 512;              // bound on TILE (+1 row read past a tile)
 
 // Geometry of a forward launch.
