@@ -63,14 +63,17 @@ FwdShape fwd_geometry(bool dyn, int64_t B, int64_t D, int64_t S);
 
 // TTT: keeps the raw x and r = 1/(1+exp(2 damping p)) of every token of the
 // run in registers, plus 2K gradient accumulators per lane: one lane per
-// thread (half the accumulators of two), 16-token runs.  Chosen by
-// measurement on MI355X at BASELINE configs[4] against 2 lanes x 8 or 16
-// tokens and 1 lane x 32 tokens (which spills).  Two look-back words per
-// thread (checkpoints every 16 tiles): the kernel is VALU-bound, and every
-// thread runs the polling code of each of its words, so fewer words per
-// thread cost fewer instructions per element (1147 against 1254 us with
-// eight words and 1177 with four, at configs[4]; one word 1145).
-using TttTile = TileGeo<1, 8, 16, 64, 2>;   // 128 tokens
+// thread (half the accumulators of two).  Measured on MI355X at BASELINE
+// configs[4] (bf16): 20-token runs 1085 us against 1131 with 16 (the
+// per-thread setup, chain, composition and reduction amortised over more
+// tokens), although at the 128-VGPR bound of two workgroups per CU the
+// compiler spills 5 registers; 18 tokens 1104 us, 22 tokens (13 spilled)
+// 1141, 24 tokens (21 spilled) 1355; 2 lanes x 8 or 16 tokens +10-20%.
+// Two look-back words per thread (checkpoints every 16 tiles): the kernel
+// is VALU-bound, and every thread runs the polling code of each of its
+// words (1147 against 1254 us with eight words, 1177 with four, at 16-token
+// runs; one word 1145).
+using TttTile = TileGeo<1, 8, 20, 64, 2>;   // 160 tokens
 int ttt_tile_tokens(bool dyn, int x_dtype);
 
 // Backward: one lane per thread (the clamp mask makes the adjoint map's A
