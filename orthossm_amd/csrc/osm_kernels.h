@@ -83,9 +83,11 @@ int ttt_tile_tokens(bool dyn, int x_dtype);
 // (checkpoints every 32 tiles) instead of eight brought the static kernel from
 // 101 to 77 VGPRs, three workgroups per CU instead of two: 129 against 141 us
 // at BASELINE configs[1] on MI355X; two words (checkpoints every 16 tiles)
-// 116.9 against 118.2 us with four.  32-token runs spill; 8-token runs are
-// slower (185 us).
-using BwdTile = TileGeo<1, 8, 16, 64, 2>;   // 128 tokens
+// 116.9 against 118.2 us with four.  24-token runs (94 VGPRs, two
+// workgroups per CU) 113.8-114.4 against 116.5-116.8 us for 16 tokens; 20
+// tokens 114.3, 28 tokens 118.2, 32 tokens 114.2; 8-token runs are slower
+// (185 us).
+using BwdTile = TileGeo<1, 8, 24, 64, 2>;   // 192 tokens
 int bwd_tile_tokens(bool dyn);
 
 // Workspace: a kHeaderBytes header (launch epoch, fault word, completion

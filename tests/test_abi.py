@@ -123,10 +123,10 @@ def test_ttt_argument_errors():
 def test_bwd_workspace_bytes_formula():
     lib = nat.load()
     a = _args()
-    # 128-token tiles (n_tiles = 128 at S=16384), two look-back words per
+    # 192-token tiles (n_tiles = 86 at S=16384), two look-back words per
     # lane, then K-padded partials per tile.
-    slots = (2048 + 32 * 128 * 64 * 16 + 255) // 256 * 256
-    assert lib.osm_workspace_bytes(ctypes.byref(a), nat.OP_BWD) == slots + 32 * 128 * 8 * 64 * 4
+    slots = (2048 + 32 * 86 * 64 * 16 + 255) // 256 * 256
+    assert lib.osm_workspace_bytes(ctypes.byref(a), nat.OP_BWD) == slots + 32 * 86 * 8 * 64 * 4
     assert lib.osm_workspace_bytes(ctypes.byref(a), 3) == 0
     assert b"osm_op" in lib.osm_last_error()
 

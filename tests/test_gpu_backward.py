@@ -47,8 +47,8 @@ def check(inp, out, gx, gc, gi, go, gs, init, **kw):
 
 @pytest.mark.parametrize("B,S,H,hd,K,dyn", [
     (1, 1, 8, 64, 8, False),         # one token
-    (2, 127, 8, 64, 8, False),       # one partial tile
-    (1, 129, 8, 64, 8, False),       # full tile + 1 token
+    (2, 191, 8, 64, 8, False),       # one partial (192-token) tile
+    (1, 193, 8, 64, 8, False),       # full tile + 1 token
     (3, 1000, 4, 32, 5, False),      # hd < 64, K padded to 8
     (1, 300, 3, 20, 8, False),       # D = 60: partial lane-block
     (2, 777, 2, 12, 3, False),       # D = 24, K <= 4 kernel
