@@ -69,11 +69,12 @@ FwdShape fwd_geometry(bool dyn, int64_t B, int64_t D, int64_t S);
 // tokens), although at the 128-VGPR bound of two workgroups per CU the
 // compiler spills 5 registers; 18 tokens 1104 us, 22 tokens (13 spilled)
 // 1141, 24 tokens (21 spilled) 1355; 2 lanes x 8 or 16 tokens +10-20%.
-// Two look-back words per thread (checkpoints every 16 tiles): the kernel
-// is VALU-bound, and every thread runs the polling code of each of its
-// words (1147 against 1254 us with eight words, 1177 with four, at 16-token
-// runs; one word 1145).
-using TttTile = TileGeo<1, 8, 20, 64, 2>;   // 160 tokens
+// One look-back word per thread (checkpoints every 8 tiles): the kernel is
+// VALU-bound, and every thread runs the polling code of each of its words
+// (at 16-token runs 1147 us with two words against 1254 with eight and 1177
+// with four; at 20-token runs one word 1069 against 1086 with two, which
+// also spills one register more).
+using TttTile = TileGeo<1, 8, 20, 64, 1>;   // 160 tokens
 int ttt_tile_tokens(bool dyn, int x_dtype);
 
 // Backward: one lane per thread (the clamp mask makes the adjoint map's A
