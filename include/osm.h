@@ -56,7 +56,11 @@
  *     one allocated at the same address must be passed through
  *     osm_workspace_init.  Two calls that overlap in time must not share one
  *     workspace; if they do, every wave still exits (bounded waits) and the
- *     header's fault word (offset 12) is set.
+ *     header's fault word (offset 12) is set to the fault tag of the launch
+ *     whose wait gave up; osm_workspace_status reads (and resets) it.  The
+ *     launch counter in the header only grows (clears on a layout change
+ *     leave it alone); one workspace serves 2^30 launches, after which it
+ *     must be passed through osm_workspace_init.
  */
 #ifndef ORTHOSSM_AMD_OSM_H
 #define ORTHOSSM_AMD_OSM_H
@@ -231,6 +235,16 @@ size_t osm_workspace_bytes(const osm_cheby_args* args, int op);
 
 /* Zero-fill `bytes` of workspace on `stream` with a fill kernel. */
 int osm_workspace_init(void* workspace, size_t bytes, void* stream);
+
+/* Stream-ordered health check of a workspace, with no host synchronisation:
+ * a one-thread kernel on `stream` writes status[0] = the header's fault word
+ * (0 if no look-back wait of a launch on this workspace has given up since
+ * the last reset, else (epoch << 2 | 3) of the last launch that did, whose
+ * results are invalid) and status[1] = the launch counter, into `status`
+ * (2 x uint32 of device memory); with reset != 0 it then clears the fault
+ * word.  No counterpart in the reference, whose tile loop
+ * (sdpc_kernel.py:2006) never waits on another workgroup. */
+int osm_workspace_status(void* workspace, uint32_t* status, int reset, void* stream);
 
 /* Fused forward.  Replaces the kernel launches listed in the header comment. */
 int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t workspace_bytes,

@@ -34,7 +34,11 @@ STATUS = {
     -4: "OSM_E_LAYOUT",
     -5: "OSM_E_WORKSPACE",
     -6: "OSM_E_HIP",
+    -7: "OSM_E_FAULT",
 }
+# Raised by the Python layer (not returned by the library) when a workspace's
+# fault word shows that a launch's look-back wait gave up.
+OSM_E_FAULT = -7
 
 # Every function the header declares; tests check the library exports each.
 EXPORTS = (
@@ -42,6 +46,7 @@ EXPORTS = (
     "osm_last_error",
     "osm_workspace_bytes",
     "osm_workspace_init",
+    "osm_workspace_status",
     "osm_cheby_ema_fwd",
     "osm_cheby_ema_ttt",
     "osm_cheby_ema_bwd",
@@ -184,6 +189,8 @@ def load() -> ctypes.CDLL:
         lib.osm_workspace_bytes.argtypes = [ctypes.POINTER(ChebyArgs), ctypes.c_int]
         lib.osm_workspace_init.restype = ctypes.c_int
         lib.osm_workspace_init.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.osm_workspace_status.restype = ctypes.c_int
+        lib.osm_workspace_status.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
         lib.osm_cheby_ema_fwd.restype = ctypes.c_int
         lib.osm_cheby_ema_fwd.argtypes = [ctypes.POINTER(ChebyArgs), ctypes.c_void_p, ctypes.c_size_t,
                                           ctypes.c_void_p]

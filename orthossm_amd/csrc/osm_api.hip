@@ -178,12 +178,15 @@ int hip_fail(hipError_t e, const char* what) {
   return fail(OSM_E_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Layout last used on each workspace.  Look-back words carry an epoch tag, so
-// a workspace can be reused without clearing as long as its layout is
-// unchanged; when the layout changes (other shape, mode or lambda kind) old
-// payloads could sit where the new layout expects tagged words, so the
-// workspace is cleared on the stream first.  A workspace seen for the first
-// time is cleared too, unless osm_workspace_init zeroed it.
+// Layout last used on each workspace.  Look-back words carry the tag of the
+// launch that wrote them and the header's launch epoch only ever grows (a
+// clear on a layout change leaves the header alone), so a word left by an
+// earlier launch, of any layout, never matches a later launch's tag: the
+// workspace needs no clear between launches.  The look-back words are still
+// cleared when the layout changes (other shape, mode or lambda kind), which
+// keeps stale payloads of another layout out of the words a launch reads.  A
+// workspace seen for the first time is cleared in full (header included),
+// unless osm_workspace_init zeroed it.
 struct Layout {
   int n_lb, n_tiles, tile, lanes, kpad;
   bool dyn;
@@ -199,15 +202,19 @@ std::unordered_map<uintptr_t, Layout> g_ws_layout;
 
 int prepare_workspace(void* ws, size_t need, const Geometry& geo, int op, hipStream_t stream) {
   const Layout now{geo.n_lb, geo.n_tiles, geo.tile, geo.lanes, geo.kpad, geo.dyn, op};
-  bool clear;
+  bool fresh, clear;
   {
     std::lock_guard<std::mutex> lk(g_ws_mu);
     auto it = g_ws_layout.find((uintptr_t)ws);
-    clear = it == g_ws_layout.end() || !(it->second == now || it->second == kZeroed);
+    fresh = it == g_ws_layout.end();
+    clear = fresh || !(it->second == now || it->second == kZeroed);
     g_ws_layout[(uintptr_t)ws] = now;
   }
   if (clear) {
-    const hipError_t e = osm::launch_fill_zero(ws, need, stream);
+    // A known workspace keeps its header (epoch, fault word): only the
+    // look-back words are cleared.
+    const size_t skip = fresh ? 0 : osm::kHeaderBytes;
+    const hipError_t e = osm::launch_fill_zero(static_cast<char*>(ws) + skip, need - skip, stream);
     if (e != hipSuccess) {
       std::lock_guard<std::mutex> lk(g_ws_mu);
       g_ws_layout.erase((uintptr_t)ws);
@@ -255,6 +262,15 @@ int osm_workspace_init(void* workspace, size_t bytes, void* stream) {
     std::lock_guard<std::mutex> lk(g_ws_mu);
     g_ws_layout[(uintptr_t)workspace] = kZeroed;
   }
+  return ok();
+}
+
+int osm_workspace_status(void* workspace, uint32_t* status, int reset, void* stream) {
+  if (!workspace) return fail(OSM_E_WORKSPACE, "workspace is NULL");
+  if ((uintptr_t)workspace % 256) return fail(OSM_E_WORKSPACE, "workspace must be 256-byte aligned");
+  if (!status || (uintptr_t)status % 4) return fail(OSM_E_ARG, "status must be a 4-byte aligned device pointer");
+  const hipError_t e = osm::launch_ws_status(workspace, status, reset ? 1 : 0, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "workspace status launch");
   return ok();
 }
 

@@ -21,8 +21,12 @@ constexpr float kTwoLog2e = 2.8853900817779268f;  // 2*log2(e): tanh via exp2
 // Workspace header (first kHeaderBytes of every workspace).
 //   epoch      launch counter; tags every published look-back word.  Read by
 //              every block at start, bumped by the last block of the launch.
-//   fault      set to 1 if a look-back wait exceeded kSpinLimit (results of
-//              that launch are invalid); only a zero fill clears it.
+//   fault      0, or the fault tag (make_tag(epoch, kKindFault)) of the last
+//              launch in which a look-back wait exceeded kSpinLimit (results
+//              of that launch are invalid).  Sticky until osm_workspace_status
+//              resets it or a full clear; a waiter gives up early only on the
+//              tag of its own launch, so an old fault does not disturb later
+//              launches.
 //   done_all   classes finished in the running launch (reset by the last one)
 //   cls[c]     per class c = blockIdx % 8 (one XCD under round-robin
 //              dispatch): `done` counts its finished blocks; the last block
@@ -52,7 +56,7 @@ constexpr unsigned kSpinLimit = 1u << 20;
 // low 32 bits = an fp32 payload.  Because tag and payload travel in one
 // atomic access, relaxed agent-scope loads/stores suffice (no fences, hence
 // no L2 write-back or invalidate on gfx950).
-enum : unsigned { kKindAgg = 1u, kKindPre = 2u };
+enum : unsigned { kKindAgg = 1u, kKindPre = 2u, kKindFault = 3u };
 
 __device__ __forceinline__ unsigned make_tag(unsigned epoch, unsigned kind) {
   return ((epoch & 0x3fffffffu) << 2) | kind;
@@ -67,24 +71,30 @@ __device__ __forceinline__ unsigned long long peek(const unsigned long long* slo
   return __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void raise_fault(unsigned* hdr_words) {
-  __hip_atomic_store(hdr_words + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Fault tag of the launch whose look-back words carry `tag` (any kind).
+__device__ __forceinline__ unsigned fault_tag_of(unsigned tag) { return (tag & ~3u) | kKindFault; }
+
+__device__ __forceinline__ void raise_fault(unsigned* hdr_words, unsigned fault_tag) {
+  __hip_atomic_store(hdr_words + 3, fault_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Spin until `slot` carries `tag`, starting from an already-loaded value.
 // The producer of every awaited word was dispatched earlier and publishes
 // without waiting on anything later (osm_chain.h), so the loop ends;
-// kSpinLimit bounds it anyway (fault flag, payload 0).
+// kSpinLimit bounds it anyway (fault word set to this launch's fault tag,
+// payload 0).
 __device__ __forceinline__ float await_word(const unsigned long long* slot, unsigned long long w, unsigned tag,
                                             unsigned* hdr_words) {
   unsigned polls = 0;
   while ((unsigned)(w >> 32) != tag) {
     ++polls;
-    // Give up when over the limit or when another wave already gave up.
+    // Give up when over the limit or when another wave of this launch
+    // already gave up (a fault left by an earlier launch is ignored).
+    const unsigned ftag = fault_tag_of(tag);
     if (polls > kSpinLimit ||
         ((polls & 1023u) == 0 &&
-         __hip_atomic_load(hdr_words + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)) {
-      raise_fault(hdr_words);
+         __hip_atomic_load(hdr_words + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ftag)) {
+      raise_fault(hdr_words, ftag);
       return 0.0f;
     }
     __builtin_amdgcn_s_sleep(1);

@@ -265,6 +265,19 @@ __global__ void fill_zero_kernel(unsigned* p, size_t n_words) {
     p[i] = 0u;
 }
 
+// Header status: dst[0] = fault word, dst[1] = launch epoch; the fault word
+// is cleared afterwards when `reset` (one thread: the read and the clear are
+// ordered by program order on one address).
+__global__ void ws_status_kernel(unsigned* hdr, unsigned* dst, int reset) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    const unsigned fault = __hip_atomic_load(hdr + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned epoch = __hip_atomic_load(hdr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    dst[0] = fault;
+    dst[1] = epoch;
+    if (reset) __hip_atomic_store(hdr + 3, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 __global__ void copy_state_kernel(const float* src, float* dst, size_t n) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
     dst[i] = src[i];
@@ -302,6 +315,11 @@ hipError_t launch_fill_zero(void* ptr, size_t bytes, hipStream_t stream) {
   if (words == 0) return hipSuccess;
   const unsigned blocks = (unsigned)std::min<size_t>((words + 255) / 256, 4096);
   hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, stream, static_cast<unsigned*>(ptr), words);
+  return hipGetLastError();
+}
+
+hipError_t launch_ws_status(void* ws, unsigned* dst, int reset, hipStream_t stream) {
+  hipLaunchKernelGGL(ws_status_kernel, dim3(1), dim3(64), 0, stream, static_cast<unsigned*>(ws), dst, reset);
   return hipGetLastError();
 }
 

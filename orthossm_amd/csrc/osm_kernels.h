@@ -199,5 +199,6 @@ hipError_t launch_bwd(const BwdParams& p, int x_dtype, int out_dtype, bool dyn, 
 hipError_t launch_v10(const V10Params& p, int x_dtype, bool use_lut, int kpad, hipStream_t stream);
 hipError_t launch_fill_zero(void* ptr, size_t bytes, hipStream_t stream);
 hipError_t launch_copy_state(const float* src, float* dst, size_t n, hipStream_t stream);
+hipError_t launch_ws_status(void* ws, unsigned* dst, int reset, hipStream_t stream);
 
 }  // namespace osm

@@ -54,7 +54,7 @@ import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint as torch_checkpoint
 
 from .ops import cheby_ema, cheby_ema_forward, head_momentum
-from .sdpc_kernel import apply_cheby_rkv_v10, v10_damping
+from .sdpc_kernel import GatedComplexityPredictor, apply_cheby_rkv_v10, v10_damping
 
 # Length routing thresholds (sdpc_engine.py:51-53).
 FAST_PATH_THRESHOLD = 384
@@ -78,19 +78,6 @@ class ChebyPathOutput(NamedTuple):
     gate: torch.Tensor             # [B,1] complexity gate
     ema_momentum: torch.Tensor     # 0-d fp32 device tensor used as mu
     route: str                     # "fast", "hybrid" or "full"
-
-
-class GatedComplexityPredictor(nn.Module):
-    """Global TTT gate from the mean input: Linear(D, D/4), SiLU,
-    Linear(D/4, 1), sigmoid (sdpc_kernel.py:1818-1830)."""
-
-    def __init__(self, d_model: int):
-        super().__init__()
-        self.net = nn.Sequential(nn.Linear(d_model, d_model // 4), nn.SiLU(), nn.Linear(d_model // 4, 1),
-                                 nn.Sigmoid())
-
-    def forward(self, x_mean: torch.Tensor) -> torch.Tensor:
-        return self.net(x_mean)
 
 
 def route(seq_len: int) -> str:

@@ -15,6 +15,7 @@ tensor that is not on a ROCm device raises.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from typing import Sequence
 
@@ -24,6 +25,59 @@ from . import _native as nat
 
 _ws_lock = threading.Lock()
 _ws_cache: dict[tuple[int, int, int], torch.Tensor] = {}
+
+# With fault checks on (environment OSM_CHECK_FAULTS=1, or set_fault_check),
+# every launch that uses a workspace is followed by a read of the workspace's
+# fault word, which synchronises the host: a look-back wait that gave up (its
+# launch's results are invalid) then raises instead of passing silently.
+_check_faults = os.environ.get("OSM_CHECK_FAULTS", "0") not in ("", "0")
+
+
+def set_fault_check(on: bool) -> bool:
+    """Turns the per-launch fault check on or off; returns the old setting."""
+    global _check_faults
+    old, _check_faults = _check_faults, bool(on)
+    return old
+
+
+def workspace_status(ws: torch.Tensor, *, reset: bool = False, stream: int | None = None) -> tuple[int, int]:
+    """(fault word, launch counter) of a workspace, read on ``stream`` (the
+    current stream of its device by default) through osm_workspace_status;
+    synchronises the host.  A non-zero fault word is the fault tag of the
+    last launch whose look-back wait gave up; ``reset`` clears it."""
+    lib = nat.load()
+    if stream is None:
+        stream = torch.cuda.current_stream(ws.device).cuda_stream
+    st = torch.empty(2, dtype=torch.int32, device=ws.device)
+    nat.check(lib.osm_workspace_status(ctypes.c_void_p(ws.data_ptr()), ctypes.c_void_p(st.data_ptr()),
+                                       1 if reset else 0, ctypes.c_void_p(stream)))
+    fault, epoch = (int(v) & 0xFFFFFFFF for v in st.cpu().tolist())
+    return fault, epoch
+
+
+def workspace_faults(reset: bool = True) -> list[tuple[tuple[int, int, int], int]]:
+    """Fault words of every workspace this module has created, as
+    [((device, stream, op), fault word)] for the non-zero ones.  Each device
+    is synchronised first and the words are read on its current stream (the
+    stream a workspace was made for may no longer exist).  ``reset`` clears
+    the words it reports."""
+    with _ws_lock:
+        items = list(_ws_cache.items())
+    bad = []
+    for key, ws in items:
+        torch.cuda.synchronize(ws.device)
+        fault, _ = workspace_status(ws, reset=reset)
+        if fault:
+            bad.append((key, fault))
+    return bad
+
+
+def _after_launch(ws: torch.Tensor, stream: int, what: str) -> None:
+    if _check_faults:
+        fault, epoch = workspace_status(ws, reset=True, stream=stream)
+        if fault:
+            raise nat.OsmError(nat.OSM_E_FAULT, f"{what}: a look-back wait gave up (fault word 0x{fault:08x}, "
+                                                f"launch counter {epoch}); the results of that launch are invalid")
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int, op: int) -> torch.Tensor:
@@ -149,6 +203,7 @@ def cheby_ema_forward(x: torch.Tensor, coeffs: torch.Tensor, damping: Sequence[f
     ws = _workspace(dev, stream, nbytes, nat.OP_FWD)
     nat.check(lib.osm_cheby_ema_fwd(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
                                     ctypes.c_void_p(stream)))
+    _after_launch(ws, stream, "osm_cheby_ema_fwd")
     del keep
     return (out, ema_final) if return_state else out
 
@@ -184,6 +239,7 @@ def cheby_ema_ttt(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, *, g: tor
     ws = _workspace(dev, stream, nbytes, nat.OP_TTT)
     nat.check(lib.osm_cheby_ema_ttt(ctypes.byref(a), ctypes.c_void_p(grad.data_ptr()), tgt,
                                     ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(stream)))
+    _after_launch(ws, stream, "osm_cheby_ema_ttt")
     del keep
     return (out, grad, ema_final) if return_state else (out, grad)
 
@@ -263,6 +319,7 @@ def cheby_ema_backward(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, out:
     ws = _workspace(dev, stream, nbytes, nat.OP_BWD)
     nat.check(lib.osm_cheby_ema_bwd(ctypes.byref(a), ctypes.byref(bw), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
                                     ctypes.c_void_p(stream)))
+    _after_launch(ws, stream, "osm_cheby_ema_bwd")
     del keep, go, gs
     return gx, gc, gi
 
@@ -315,8 +372,27 @@ def cheby_ema(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, *, g: torch.T
 # Per-head Lion forget factors of the reference (MULTI_SCALE_LAMBDA,
 # sdpc_kernel.py:1416); heads past the eighth use 0.995 (1429-1432).
 V10_LION_LAMBDA = (0.9995, 0.9995, 0.997, 0.997, 0.995, 0.995, 0.97, 0.95)
+# Half-table of the full path's LUT mode: points on [0, 1], terms T_0..T_7
+# (sdpc_kernel.py:58-59).
+LUT_POINTS = 256
+LUT_TERMS = 8
 _v10_lock = threading.Lock()
 _v10_cache: dict = {}
+
+
+def chebyshev_lut_table(points: int = LUT_POINTS, terms: int = LUT_TERMS) -> torch.Tensor:
+    """[terms, points] fp32 CPU tensor: T_k on ``torch.linspace(0, 1, points)``
+    by the three-term recurrence T_k = 2u T_{k-1} - T_{k-2} in fp32, the
+    construction the kernels' table values must reproduce bit for bit
+    (sdpc_kernel.py:63-81)."""
+    grid = torch.linspace(0.0, 1.0, points)
+    T = torch.zeros(terms, points)
+    T[0] = 1.0
+    if terms > 1:
+        T[1] = grid
+    for k in range(2, terms):
+        T[k] = 2.0 * grid * T[k - 1] - T[k - 2]
+    return T
 
 
 def v10_tables(device: torch.device, n_heads: int, K: int):
@@ -329,12 +405,7 @@ def v10_tables(device: torch.device, n_heads: int, K: int):
         hit = _v10_cache.get(key)
         if hit is not None:
             return hit
-        grid = torch.linspace(0.0, 1.0, 256)
-        T = torch.zeros(8, 256)
-        T[0] = 1.0
-        T[1] = grid
-        for k in range(2, 8):
-            T[k] = 2.0 * grid * T[k - 1] - T[k - 2]
+        T = chebyshev_lut_table()
         n_active = min(n_heads, len(V10_LION_LAMBDA))
         lam = torch.tensor(list(V10_LION_LAMBDA[:n_active]) + [0.995] * max(0, n_heads - n_active))
         ss = 1.0 / (torch.arange(K, dtype=torch.float32) + 1.0) ** 1.5

@@ -23,12 +23,106 @@ at every chunk, bf16 rounding of x and of the output) runs as one launch of
 ``v10_chunked_ttt``; with gradients enabled, through ``v10_full_path``,
 whose backward is the reference's (FusedChebyRKVv10.backward,
 sdpc_kernel.py:2436-2515) on every chunk.
+
+The module also carries the other names the reference's callers import from
+``sdpc_kernel`` together with the op (sdpc_engine.py:39-43,
+chimera_experiment/chimera_v2_ssm.py:54, pretrain_real.py:211,
+benchmark_ortho.py:20, model.py:20, benchmark_ruler_pg19.py:30,
+precision_tests.py:33, ortho_diagnostics.py:174): the spectral coefficient
+initialisation ``init_chebyshev_coefficients``, the complexity gate module
+``GatedComplexityPredictor``, the LUT accessor ``get_chebyshev_lut`` with
+``LUT_TABLE_SIZE`` and ``MAX_DEGREE``, and ``MULTI_SCALE_LAMBDA``.  The
+reference's Triton kernel objects (``_fused_clenshaw_ema_kernel``) have no
+counterpart: their launches are the C ABI's entry points.
 """
 from __future__ import annotations
 
-import torch
+import math
+import threading
 
-from .ops import cheby_ema, cheby_ema_forward, head_momentum, v10_chunked_ttt, v10_full_path
+import torch
+import torch.nn as nn
+
+from .ops import (LUT_POINTS, LUT_TERMS, V10_LION_LAMBDA, cheby_ema, cheby_ema_forward, chebyshev_lut_table,
+                  head_momentum, v10_chunked_ttt, v10_full_path)
+
+# Points of the full path's half-table LUT and the number of Chebyshev terms
+# it holds (sdpc_kernel.py:58-59).
+LUT_TABLE_SIZE: int = LUT_POINTS
+MAX_DEGREE: int = LUT_TERMS
+# Per-head Lion forget factors of the full path, heads 0..7 (sdpc_kernel.py:1416).
+MULTI_SCALE_LAMBDA = list(V10_LION_LAMBDA)
+
+_lut_lock = threading.Lock()
+_lut_by_device: dict = {}
+
+
+def get_chebyshev_lut(device) -> torch.Tensor:
+    """The [MAX_DEGREE, LUT_TABLE_SIZE] fp32 Chebyshev half-table on
+    ``device`` (T_k on linspace(0, 1, 256), fp32 recurrence), built once per
+    device under a lock (sdpc_kernel.py:84-96).  The full path's kernels read
+    the same table."""
+    key = torch.device(device)
+    hit = _lut_by_device.get(key)
+    if hit is None:
+        with _lut_lock:
+            hit = _lut_by_device.get(key)
+            if hit is None:
+                hit = chebyshev_lut_table().to(key).contiguous()
+                _lut_by_device[key] = hit
+    return hit
+
+
+class GatedComplexityPredictor(nn.Module):
+    """Global TTT gate from the mean input: Linear(D, D/4), SiLU,
+    Linear(D/4, 1), sigmoid (sdpc_kernel.py:1818-1830).  The module layout
+    (``net.0``, ``net.2``) is the reference's, so its state_dict entries load."""
+
+    def __init__(self, d_model: int):
+        super().__init__()
+        self.net = nn.Sequential(nn.Linear(d_model, d_model // 4), nn.SiLU(), nn.Linear(d_model // 4, 1),
+                                 nn.Sigmoid())
+
+    def forward(self, x_mean: torch.Tensor) -> torch.Tensor:
+        return self.net(x_mean)
+
+
+def init_chebyshev_coefficients(batch: int, n_heads: int, degree: int, head_dim: int, device) -> torch.Tensor:
+    """Initial coefficients [batch, n_heads, degree, head_dim] fp32
+    (sdpc_kernel.py:1833-1867).
+
+    One standard-normal draw of that shape (the same call on the torch
+    generator as the reference, so a seeded run draws the same numbers),
+    scaled per term by sigma_k = 0.1/(k+1).  With two or more heads, each
+    batch row's heads are then decorrelated, treating head h as the row
+    vector of its degree*head_dim coefficients:
+
+    * degree*head_dim >= n_heads: the rows are replaced by the orthonormal
+      basis that QR (Gram-Schmidt order, head 0 first) gives for them, each
+      rescaled to its original norm, so the rows become mutually orthogonal
+      and keep their lengths;
+    * degree*head_dim < n_heads (more heads than dimensions, so no
+      orthogonal set exists): the norm-1 rows are replaced by their polar
+      factor U V^T (the nearest matrix with orthonormal columns) times
+      sqrt(n_heads / (degree*head_dim)), a Parseval tight frame, and each row
+      is rescaled to its original norm.
+    """
+    k = torch.arange(degree, device=device, dtype=torch.float32)
+    sigma = (0.1 / (k + 1.0)).view(1, 1, degree, 1)
+    coeffs = torch.randn(batch, n_heads, degree, head_dim, device=device) * sigma
+    if n_heads < 2:
+        return coeffs
+    width = degree * head_dim
+    rows = coeffs.view(batch, n_heads, width)
+    norms = rows.norm(dim=2, keepdim=True)
+    if width >= n_heads:
+        q, _ = torch.linalg.qr(rows.transpose(1, 2))        # [batch, width, n_heads]
+        out = q.transpose(1, 2) * norms
+    else:
+        unit = rows / (norms + 1e-8)
+        u, _, vh = torch.linalg.svd(unit, full_matrices=False)
+        out = (u @ vh) * math.sqrt(n_heads / width) * norms
+    return out.reshape(batch, n_heads, degree, head_dim)
 
 
 def v10_damping(n_heads: int, device=None) -> torch.Tensor:

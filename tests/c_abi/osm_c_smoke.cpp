@@ -3,7 +3,8 @@
 // memory, checked against a double-precision restatement in plain loops of
 // the reference's fixed-coefficient path (sdpc_kernel.py:1722-1739: softsign,
 // Chebyshev series, damping, tanh; the per-head EMA of chimera_v2_ssm.py:
-// 86-101, clamped as the reference's scan does), then one argument error.
+// 86-101, clamped as the reference's scan does), the workspace's fault word
+// and launch counter, then one argument error.
 // Built by orthossm_amd/build.py; run by tests/test_gpu_c_abi.py.  Prints
 // "ok ..." and exits 0 on success.
 #include <hip/hip_runtime_api.h>
@@ -123,6 +124,19 @@ int main(void) {
   }
   const double rel = max_err / max_ref;
 
+  // The workspace header after the two launches: no look-back wait gave up
+  // (fault word 0) and the launch counter went 0 -> 2.
+  uint32_t* dstatus;
+  uint32_t status[2] = {0xffffffffu, 0u};
+  HIP_OK(hipMalloc((void**)&dstatus, sizeof(status)));
+  if (osm_workspace_status(ws, dstatus, 1, NULL) != OSM_OK) {
+    fprintf(stderr, "osm_workspace_status: %s\n", osm_last_error());
+    return 1;
+  }
+  HIP_OK(hipMemcpy(status, dstatus, sizeof(status), hipMemcpyDeviceToHost));
+  hipFree(dstatus);
+  const int status_ok = status[0] == 0u && status[1] == 2u;
+
   // Argument errors come back as status codes, before any HIP call.
   osm_cheby_args bad = a;
   bad.K = OSM_MAX_K + 1;
@@ -131,10 +145,12 @@ int main(void) {
 
   hipFree(ws); hipFree(dx); hipFree(dout); hipFree(dc); hipFree(ddamp); hipFree(dlam);
   free(x); free(out); free(c); free(ref);
-  if (!(rel <= 1e-5) || !err_ok) {
-    fprintf(stderr, "FAILED: max rel err %.3e (limit 1e-5), bad-K status %d\n", rel, rc_bad);
+  if (!(rel <= 1e-5) || !err_ok || !status_ok) {
+    fprintf(stderr, "FAILED: max rel err %.3e (limit 1e-5), bad-K status %d, fault word 0x%08x, launches %u\n",
+            rel, rc_bad, status[0], status[1]);
     return 1;
   }
-  printf("ok: C ABI forward max rel err %.3e over %zu elements; bad K -> status %d\n", rel, nx, rc_bad);
+  printf("ok: C ABI forward max rel err %.3e over %zu elements; bad K -> status %d; fault word 0, %u launches\n",
+         rel, nx, rc_bad, status[1]);
   return 0;
 }

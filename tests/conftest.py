@@ -30,3 +30,16 @@ def dev():
     from orthossm_amd import _native
     _native.load()
     return torch.device("cuda", 0)
+
+
+@pytest.fixture(autouse=True)
+def _no_lookback_fault(request):
+    """After every GPU test: no workspace the test used reports a look-back
+    wait that gave up (the header's fault word, read through
+    osm_workspace_status)."""
+    yield
+    if request.node.get_closest_marker("gpu") is None or not gpu_available():
+        return
+    from orthossm_amd import ops
+    bad = ops.workspace_faults(reset=True)
+    assert not bad, f"look-back fault word set after {request.node.nodeid}: {bad}"

@@ -63,3 +63,23 @@ def assert_close_grad(got, want, rtol=GRAD_RTOL, what="grad"):
     want = np.asarray(want, dtype=np.float64)
     scale = float(np.max(np.abs(want))) if want.size else 0.0
     assert_close_fp32(got, want, rtol=rtol, atol=1e-4 * scale + 1e-30, what=what)
+
+
+def compare_v10(out, cn, mn, want):
+    """The full path (out, coeffs, momentum) against oracle/v10_full.py's
+    (out, coeffs, momentum).  out holds bf16 values: equal except where fp32
+    and float64 rounding of s land on two sides of a bf16 rounding boundary
+    (one bf16 ulp).  A Lion sign that rounding decides (|interp| ~ 1e-7)
+    moves one coefficient by 2 lr ss_k, so a tiny fraction of coefficient
+    and momentum elements may differ."""
+    wo, wc, wm = want
+    o = out.cpu().numpy().astype(np.float64)
+    diff = np.abs(o - wo)
+    assert np.nanmax(np.where(np.isnan(wo), 0, diff)) <= 2e-2, "out beyond 2e-2"
+    assert (diff > 1e-6).mean() <= 1e-3, f"{(diff > 1e-6).mean():.4f} of out differ"
+    for got, w, what in ((cn, wc, "coeffs"), (mn, wm, "momentum")):
+        g = got.cpu().numpy().astype(np.float64)
+        both = np.isnan(g) & np.isnan(w)
+        d = np.abs(np.where(both, 0, g) - np.where(both, 0, w))
+        assert not np.isnan(d).any(), f"{what}: NaN mismatch"
+        assert (d > 1e-5 * (1 + np.abs(w))).mean() <= 1e-3, f"{what}: {(d > 1e-5).sum()} elements off"

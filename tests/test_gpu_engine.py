@@ -1,12 +1,21 @@
 """The engine's Cheby-RKV call sites on the GPU (orthossm_amd/engine.py):
-each route gives exactly what a direct call of the drop-in with the engine's
-arguments gives (the reference engine's call, sdpc_engine.py:239-333, with
-mu passed as a float), the device-resident mu equals the float one bit for
-bit, a forward makes no host synchronisation, the EMA carry continues one
-scan across calls, and activation checkpointing leaves the gradients
-unchanged."""
+each route matches the CPU oracle fed with the engine's host steps restated
+in float64 (input norm, coefficient init, complexity gate, mu schedule;
+sdpc_engine.py:163-225, 239-333), each route gives exactly what a direct call
+of the drop-in with the engine's arguments gives (mu passed as a float), the
+device-resident mu equals the float one bit for bit, a forward makes no host
+synchronisation, the EMA carry continues one scan across calls, and
+activation checkpointing leaves the gradients unchanged."""
+import math
+
+import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
+
+from helpers import assert_close_fp32, compare_v10
+from oracle import cheby_ema as O
+from oracle import v10_full as V
 
 from orthossm_amd import apply_cheby_rkv_v10
 from orthossm_amd import engine as E
@@ -39,6 +48,64 @@ def direct(m, x, state, mu, tier):
     thr = E.FAST_PATH_THRESHOLD if tier == "fast" else 0
     return apply_cheby_rkv_v10(xn, c, mom, n_heads=H, base_lr=0.005, ema_momentum=mu, gate_global=gate,
                                dynamic_lambda=gate, use_lut=True, seq_threshold=thr)
+
+
+def host_steps_f64(m, x, tokens_before):
+    """The engine's steps before its apply_cheby_rkv_v10 call, in float64 on
+    the CPU from the module's weights (sdpc_engine.py:163-209): RMSNorm with
+    eps = fp32 machine epsilon, mean over tokens, coefficients
+    coeff_init_proj(mean) * 0.1/(k+1), gate sigmoid(MLP(mean)), and mu =
+    0.7 + 0.5 (ema_base - 0.7)(1 + cos(pi p)), p = min(tokens/1e8, 1) after
+    adding this call's tokens.  Returns (x_normed, coeffs, gate [B], mu)."""
+    W = {k: v.detach().cpu().double() for k, v in m.state_dict().items()}
+    xd = x.detach().cpu().double()
+    B, S, _ = xd.shape
+    eps = torch.finfo(torch.float32).eps
+    xn = xd * torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + eps) * W["input_norm.weight"]
+    xm = xn.mean(dim=1)
+
+    def mlp(prefix, v):
+        hid = F.silu(v @ W[f"{prefix}.0.weight"].T + W[f"{prefix}.0.bias"])
+        return hid @ W[f"{prefix}.2.weight"].T + W[f"{prefix}.2.bias"]
+
+    k = torch.arange(K, dtype=torch.float64)
+    c = mlp("coeff_init_proj", xm).view(B, H, K, D // H) * (0.1 / (k + 1.0)).view(1, 1, K, 1)
+    gate = torch.sigmoid(mlp("complexity_gate.net", xm)).reshape(B)
+    p = min((tokens_before + S) / 1e8, 1.0)
+    mu = 0.7 + 0.5 * (float(W["ema_base"]) - 0.7) * (1.0 + math.cos(math.pi * p))
+    return xn, c, gate, mu
+
+
+@pytest.mark.parametrize("S,tier,tokens_before", [(200, "fast", 0), (300, "fast", 37_000_000),
+                                                  (600, "hybrid", 0), (1100, "full", 80_000_000)])
+def test_routes_match_oracle(dev, S, tier, tokens_before):
+    m = make(dev, seed=S)
+    with torch.no_grad():
+        m.input_norm.weight.uniform_(0.5, 1.5, generator=torch.Generator(device=dev).manual_seed(S))
+        m.total_tokens_seen.fill_(tokens_before)
+    x = torch.randn(2, S, D, generator=torch.Generator().manual_seed(S + 1)) * 1.7
+    with torch.no_grad():
+        r = m(x.to(dev))
+    torch.cuda.synchronize()
+    assert r.route == tier
+    xn, c, gate, mu = host_steps_f64(m, x, tokens_before)
+    assert abs(float(r.ema_momentum) - mu) <= 1e-7
+    assert_close_fp32(r.x_normed.cpu(), xn.numpy(), what="x_normed")
+    assert_close_fp32(r.gate.reshape(-1).cpu(), gate.numpy(), what="gate")
+    if tier == "fast":
+        # the fixed-coefficient path: V10 damping 0.98 - 0.06 h/H, mu on every
+        # head, NaN as u = 0 (sdpc_kernel.py:1708-1744)
+        damping = 0.98 - 0.06 * np.arange(H) / H
+        want, _ = O.forward(xn.numpy(), c.numpy(), damping, np.full(H, mu), nan_policy="zero_u")
+        assert_close_fp32(r.out.cpu(), want)
+        assert_close_fp32(r.state[0].cpu(), c.numpy(), what="coeffs")
+        assert torch.count_nonzero(r.state[1]) == 0
+    else:
+        # the full path with the gate as gate_global and dynamic_lambda
+        want = V.v10_full(xn.float().numpy(), c.numpy(), np.zeros(c.shape), n_heads=H, base_lr=0.005,
+                          ema_momentum=mu, gate_global=gate.numpy(), dynamic_lambda=gate.numpy(), use_lut=True,
+                          chunk_size=256)
+        compare_v10(r.out, r.state[0], r.state[1], want)
 
 
 @pytest.mark.parametrize("S,tier", [(200, "fast"), (600, "hybrid"), (1100, "full")])

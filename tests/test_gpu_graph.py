@@ -115,3 +115,34 @@ def test_full_path_graph_replays_match_eager(dev):
         torch.cuda.synchronize()
         for got, w, what in zip(res[0], want, ("out", "coeffs", "momentum")):
             assert torch.equal(got, w), f"replay {i} {what}"
+
+
+def test_forward_graph_with_other_layouts_on_the_capture_stream(dev):
+    # Between replays an eager call of another shape runs on the capture
+    # stream, so on the same workspace with another layout (the library
+    # clears its look-back words).  The captured launch then reuses the
+    # workspace with no host step; the inputs change before every replay, so
+    # a look-back word left by an earlier replay (another payload) that
+    # matched a later launch's tag would give a wrong result.
+    big = [to_dev(inputs(2, 6000, 8, 64, seed=40 + i), dev) for i in range(4)]
+    small = to_dev(inputs(1, 700, 8, 64, seed=39), dev)
+    xbuf = big[0]["x"].clone()
+    c, damp, lam = big[0]["coeffs"], big[0]["damping"], big[0]["lam"]
+    out = torch.empty_like(xbuf)
+    cap = torch.cuda.Stream()
+
+    def step():
+        cheby_ema_forward(xbuf, c, damp, lam, out=out)
+
+    g = _capture(step, cap)
+    for i in range(4):
+        xbuf.copy_(big[i]["x"])
+        want = cheby_ema_forward(xbuf, c, damp, lam)        # default stream, its own workspace
+        torch.cuda.synchronize()
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"
+        with torch.cuda.stream(cap):
+            cheby_ema_forward(small["x"][:, : 300 + 100 * i], small["coeffs"], small["damping"], small["lam"])
+        torch.cuda.synchronize()

@@ -4,6 +4,7 @@ import numpy as np
 import pytest
 import torch
 
+from helpers import compare_v10 as compare
 from oracle import v10_full as V
 from orthossm_amd import apply_cheby_rkv_v10
 from orthossm_amd.ops import v10_chunked_ttt
@@ -17,25 +18,6 @@ def case(B, S, H, hd, K, seed, mom_scale=0.0):
     c = torch.randn(B, H, K, hd, generator=gen) / torch.arange(1, K + 1).view(1, 1, K, 1)
     m = torch.randn(B, H, K, hd, generator=gen) * mom_scale
     return x, c, m
-
-
-def compare(out, cn, mn, want):
-    wo, wc, wm = want
-    o = out.cpu().numpy().astype(np.float64)
-    # out holds bf16 values: equal except where fp32/fp64 rounding of s lands
-    # on the other side of a bf16 rounding boundary (one bf16 ulp).
-    diff = np.abs(o - wo)
-    assert np.nanmax(np.where(np.isnan(wo), 0, diff)) <= 2e-2, "out beyond 2e-2"
-    assert (diff > 1e-6).mean() <= 1e-3, f"{(diff > 1e-6).mean():.4f} of out differ"
-    # coefficients/momentum: fp32 against float64; a Lion sign decided by
-    # rounding (|interp| ~ 1e-7) moves one coefficient by 2 lr ss_k, so allow
-    # a tiny fraction of such elements.
-    for got, w, what in ((cn, wc, "coeffs"), (mn, wm, "momentum")):
-        g = got.cpu().numpy().astype(np.float64)
-        both = np.isnan(g) & np.isnan(w)
-        d = np.abs(np.where(both, 0, g) - np.where(both, 0, w))
-        assert not np.isnan(d).any(), f"{what}: NaN mismatch"
-        assert (d > 1e-5 * (1 + np.abs(w))).mean() <= 1e-3, f"{what}: {(d > 1e-5).sum()} elements off"
 
 
 def oracle(x, c, m, **kw):
@@ -197,3 +179,39 @@ def test_v10_batch_row_beyond_2gib(dev):
     for u, v in zip(a, b):
         assert torch.equal(u, v)
     del x_big
+
+
+def mismatch_fractions(out, cn, mn, want):
+    """(fraction of out elements off by > 1e-6, fraction of coefficient and
+    momentum elements off by > 1e-5 (1 + |want|)) of one comparison."""
+    wo, wc, wm = want
+    o = out.cpu().numpy().astype(np.float64)
+    f_out = float((np.abs(o - wo) > 1e-6).mean())
+    f_cm = []
+    for got, w in ((cn, wc), (mn, wm)):
+        g = got.cpu().numpy().astype(np.float64)
+        f_cm.append(float((np.abs(g - w) > 1e-5 * (1 + np.abs(w))).mean()))
+    return f_out, max(f_cm)
+
+
+def test_v10_bench_shape_rows_match_oracle(dev):
+    """The workload bench.py times for the full path: B=4 S=16384 D=512 H=8
+    K=8, 64 chunks of 256 tokens with the Lion update between them, LUT
+    series, the bench's inputs (zero momentum).  Batch rows 0 and 3 are each
+    compared with the float64 oracle run on that row (rows are independent).
+    Lion steps whose sign rounding decides (|interp| near 0) can differ
+    between fp32 and float64 and then move later outputs of that lane; the
+    measured fractions are printed and held under the budget of ``compare``."""
+    from orthossm_amd.synthetic import CONFIGS, make_config_inputs
+    cfg = CONFIGS["v10_full"]
+    inp = make_config_inputs(cfg)
+    x, c = inp["x"], inp["coeffs"]
+    m = torch.zeros_like(c)
+    out, cn, mn = v10_chunked_ttt(x.to(dev), c.to(dev), m.to(dev), n_heads=cfg.H, chunk_size=cfg.v10)
+    torch.cuda.synchronize()
+    for b in (0, cfg.B - 1):
+        want = oracle(x[b:b + 1], c[b:b + 1], m[b:b + 1], n_heads=cfg.H, chunk_size=cfg.v10)
+        f_out, f_cm = mismatch_fractions(out[b:b + 1], cn[b:b + 1], mn[b:b + 1], want)
+        print(f"v10 bench shape row {b}: out mismatch fraction {f_out:.2e}, "
+              f"coeffs/momentum mismatch fraction {f_cm:.2e}", flush=True)
+        compare(out[b:b + 1], cn[b:b + 1], mn[b:b + 1], want)
