@@ -242,13 +242,30 @@ int osm_workspace_init(void* workspace, size_t bytes, void* stream);
  * the last reset, else (epoch << 2 | 3) of the last launch that did, whose
  * results are invalid) and status[1] = the launch counter, into `status`
  * (2 x uint32 of device memory); with reset != 0 it then clears the fault
- * word.  No counterpart in the reference, whose tile loop
+ * word.  workspace = NULL reads the static scratch of
+ * osm_cheby_ema_fwd_static on the current device (after that entry point
+ * has run there).  No counterpart in the reference, whose tile loop
  * (sdpc_kernel.py:2006) never waits on another workgroup. */
 int osm_workspace_status(void* workspace, uint32_t* status, int reset, void* stream);
 
 /* Fused forward.  Replaces the kernel launches listed in the header comment. */
 int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t workspace_bytes,
                       void* stream);
+
+/* The fused forward of osm_cheby_ema_fwd with no workspace argument and no
+ * allocation: its look-back words and header live in a static device array
+ * of the library (32 MiB on every GPU it runs on, held until the process
+ * ends), set up on the first call on a device.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Results
+ * are those of osm_cheby_ema_fwd bit for bit.  Shapes whose workspace
+ * (osm_workspace_bytes) exceeds 32 MiB return OSM_E_WORKSPACE.  `stream`
+ * must belong to the current device.  Every call on one GPU shares that
+ * GPU's array: calls that overlap in time on one GPU (other streams, other
+ * threads) race, and must be ordered by the caller.  The array keeps the
+ * last call's state (launch counter, look-back words), as a workspace does;
+ * osm_workspace_status(NULL, ...) reads its fault word. */
+int osm_cheby_ema_fwd_static(const osm_cheby_args* args, void* stream);
 
 /* Fused forward + TTT coefficient gradient.  `grad` is [B,H,K,hd] fp32
  * contiguous and is overwritten.  `target` is an osm_ttt_target. */

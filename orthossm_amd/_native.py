@@ -48,6 +48,7 @@ EXPORTS = (
     "osm_workspace_init",
     "osm_workspace_status",
     "osm_cheby_ema_fwd",
+    "osm_cheby_ema_fwd_static",
     "osm_cheby_ema_ttt",
     "osm_cheby_ema_bwd",
     "osm_v10_chunked_ttt",
@@ -194,6 +195,8 @@ def load() -> ctypes.CDLL:
         lib.osm_cheby_ema_fwd.restype = ctypes.c_int
         lib.osm_cheby_ema_fwd.argtypes = [ctypes.POINTER(ChebyArgs), ctypes.c_void_p, ctypes.c_size_t,
                                           ctypes.c_void_p]
+        lib.osm_cheby_ema_fwd_static.restype = ctypes.c_int
+        lib.osm_cheby_ema_fwd_static.argtypes = [ctypes.POINTER(ChebyArgs), ctypes.c_void_p]
         lib.osm_cheby_ema_ttt.restype = ctypes.c_int
         lib.osm_cheby_ema_ttt.argtypes = [ctypes.POINTER(ChebyArgs), ctypes.c_void_p, ctypes.c_int,
                                           ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]

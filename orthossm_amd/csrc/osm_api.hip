@@ -11,6 +11,15 @@
 #include "osm.h"
 #include "osm_kernels.h"
 
+// The forward's workspace for osm_cheby_ema_fwd_static: a file-scope device
+// array, so that entry point allocates nothing.  Every GPU the library runs
+// on holds its own copy (at its own address) until the process ends.  In
+// host code `scratch` names a host-side stand-in, not device memory: its
+// device address comes from hipGetSymbolAddress, once per device, and only
+// that address is ever passed to a kernel or a fill.
+constexpr size_t kStaticScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
 namespace {
 
 thread_local std::string g_err;
@@ -224,6 +233,38 @@ int prepare_workspace(void* ws, size_t need, const Geometry& geo, int op, hipStr
   return OSM_OK;
 }
 
+// Per-device state of the static scratch, in fixed storage (no allocation
+// on the entry point's path): its device address, and the layout of the
+// last launch on it (clears follow the rules of prepare_workspace).
+constexpr int kMaxDevices = 64;
+struct StaticScratch {
+  void* ptr;
+  bool used;       // a launch has run on it (else the first one clears it in full)
+  Layout layout;   // layout of the last launch
+};
+StaticScratch g_static[kMaxDevices];
+std::mutex g_static_mu;
+
+// Device address of the current device's scratch, set up on its first use
+// with that device current.  Returns OSM_OK or an error status.
+int static_scratch_ptr(int* dev_out, void** ptr_out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(OSM_E_ARG, "device %d beyond the %d the static scratch serves", dev,
+                                                 kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_static_mu);
+  if (!g_static[dev].ptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    g_static[dev].ptr = p;
+  }
+  *dev_out = dev;
+  *ptr_out = g_static[dev].ptr;
+  return OSM_OK;
+}
+
 // S == 0 (or B == 0): nothing to compute; the final state equals the initial one.
 int run_empty(const osm_cheby_args* a, hipStream_t stream) {
   if (a->B > 0 && a->ema_final) {
@@ -266,7 +307,15 @@ int osm_workspace_init(void* workspace, size_t bytes, void* stream) {
 }
 
 int osm_workspace_status(void* workspace, uint32_t* status, int reset, void* stream) {
-  if (!workspace) return fail(OSM_E_WORKSPACE, "workspace is NULL");
+  if (!workspace) {
+    // The static scratch of osm_cheby_ema_fwd_static on the current device.
+    int dev;
+    const int rc = static_scratch_ptr(&dev, &workspace);
+    if (rc != OSM_OK) return rc;
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    if (!g_static[dev].used)
+      return fail(OSM_E_WORKSPACE, "workspace is NULL and osm_cheby_ema_fwd_static has not run on device %d", dev);
+  }
   if ((uintptr_t)workspace % 256) return fail(OSM_E_WORKSPACE, "workspace must be 256-byte aligned");
   if (!status || (uintptr_t)status % 4) return fail(OSM_E_ARG, "status must be a 4-byte aligned device pointer");
   const hipError_t e = osm::launch_ws_status(workspace, status, reset ? 1 : 0, static_cast<hipStream_t>(stream));
@@ -287,6 +336,48 @@ int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t worksp
   if (rc != OSM_OK) return rc;
   const osm::FwdParams p = make_params(args, geo, workspace);
   const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, osm::FwdShape{geo.tile, geo.lanes}, geo.kpad, st);
+  if (e != hipSuccess) return hip_fail(e, "forward kernel launch");
+  return ok();
+}
+
+int osm_cheby_ema_fwd_static(const osm_cheby_args* args, void* stream) {
+  Geometry geo;
+  int rc = check_args(args, &geo, OSM_OP_FWD);
+  if (rc != OSM_OK) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (geo.empty) return run_empty(args, st);
+  const size_t need = osm::fwd_workspace_bytes(geo.n_lb, geo.n_tiles, geo.lanes, geo.dyn);
+  if (need > kStaticScratchBytes)
+    return fail(OSM_E_WORKSPACE,
+                "this shape needs %zu bytes of look-back workspace; the static scratch holds %zu "
+                "(use osm_cheby_ema_fwd with a caller workspace)",
+                need, kStaticScratchBytes);
+  int dev;
+  void* ws;
+  rc = static_scratch_ptr(&dev, &ws);
+  if (rc != OSM_OK) return rc;
+  const Layout now{geo.n_lb, geo.n_tiles, geo.tile, geo.lanes, geo.kpad, geo.dyn, OSM_OP_FWD};
+  size_t skip = 0;
+  bool clear;
+  {
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    StaticScratch& sc = g_static[dev];
+    clear = !sc.used || !(sc.layout == now);
+    skip = sc.used ? osm::kHeaderBytes : 0;   // a used scratch keeps its header (launch counter)
+    sc.used = true;
+    sc.layout = now;
+  }
+  if (clear) {
+    const hipError_t e = osm::launch_fill_zero(static_cast<char*>(ws) + skip, need - skip, st);
+    if (e != hipSuccess) {
+      std::lock_guard<std::mutex> lk(g_static_mu);
+      g_static[dev].used = false;
+      return hip_fail(e, "static scratch clear launch");
+    }
+  }
+  const osm::FwdParams p = make_params(args, geo, ws);
+  const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, osm::FwdShape{geo.tile, geo.lanes},
+                                       geo.kpad, st);
   if (e != hipSuccess) return hip_fail(e, "forward kernel launch");
   return ok();
 }

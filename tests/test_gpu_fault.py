@@ -70,7 +70,6 @@ def test_status_argument_errors(dev):
     lib = nat.load()
     import ctypes
     st = torch.empty(2, dtype=torch.int32, device=dev)
-    assert lib.osm_workspace_status(None, ctypes.c_void_p(st.data_ptr()), 0, None) == -5
     ws = torch.zeros(4096, dtype=torch.uint8, device=dev)
     assert lib.osm_workspace_status(ctypes.c_void_p(ws.data_ptr() + 4), ctypes.c_void_p(st.data_ptr()), 0,
                                     None) == -5
