@@ -14,10 +14,12 @@ bytes per launch (every input read once, every output written once) / the
 average launch duration over that region (a step is one launch, or one per
 chunk for the streaming workload; the TTT step's two small merge kernels,
 ~2% of it, are counted in).  ``traffic`` is the HBM bytes per launch of the
-main kernel measured with rocprofv3 counters (profiles/hbm_traffic.json).
-``cpu_baseline`` times the CPU restatement of the reference's PyTorch path
-(oracle/reference_form.py) on this host's cores, on a bounded sample (one
-batch row).
+main kernel measured with rocprofv3's TCC->EA read and write request
+counters, by request size (profiles/hbm_traffic.json, written by
+``--pmc-summary``).  ``cpu_baseline`` times the CPU restatement of the
+reference's PyTorch path (oracle/reference_form.py) on this host's cores:
+for the forward workloads BASELINE configs[0] and the workload in full,
+otherwise one batch row; median of 3 runs after a warm-up.
 """
 from __future__ import annotations
 
@@ -65,48 +67,89 @@ def algorithmic_bytes(cfg) -> int:
     return total
 
 
+def cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo (the machine type if absent)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.machine()
+
+
+def _median_time(run, reps: int = 3) -> float:
+    """Median wall time of ``reps`` runs after one untimed warm-up run."""
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
 def cpu_baseline(cfg):
-    """Reference-form CPU path on one batch row of the workload."""
+    """The CPU restatement of the reference's PyTorch path on this host's
+    cores, median of 3 runs after one warm-up.  Forward workloads: BASELINE
+    configs[0] in full and the workload itself in full (the forward
+    workloads at most 2^26 elements, a few seconds per run); the other
+    workloads: one batch row of at most 16384 tokens."""
     from oracle import reference_form as RF
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     inp = make_config_inputs(cfg)
-    x = inp["x"][0:1].float()
-    c = inp["coeffs"][0:1]
-    S = min(cfg.S, 16384)
-    x = x[:, :S].contiguous()
+    forward_only = not (cfg.v10 or cfg.bwd or cfg.ttt)
+    full = forward_only and cfg.B * cfg.S * cfg.D <= (1 << 26)
+    if full:
+        x, c, lam, g = inp["x"].float(), inp["coeffs"], inp["lam"], inp["g"]
+        S = cfg.S
+    else:
+        S = min(cfg.S, 16384)
+        x = inp["x"][0:1, :S].float().contiguous()
+        c = inp["coeffs"][0:1]
+        lam, g = inp["lam"], None if inp["g"] is None else inp["g"][0:1, :S]
+    rows = x.shape[0]
     if cfg.v10:
         from oracle import v10_full as V
-        xs1, cs1 = x[:, :S].numpy(), c.double().numpy()
+        xs1, cs1 = x.numpy(), c.double().numpy()
         run = lambda: V.v10_full(xs1, cs1, 0.0 * cs1, n_heads=cfg.H, chunk_size=cfg.v10)   # noqa: E731
         what = "the full path restated in float64 numpy (oracle/v10_full.py), LUT series"
     elif cfg.bwd:
-        out, _ = RF.forward(x, c, inp["damping"], inp["lam"])
+        out, _ = RF.forward(x, c, inp["damping"], lam)
         go = torch.randn(x.shape, generator=torch.Generator().manual_seed(1))
-        run = lambda: RF.backward(x, c, inp["damping"], inp["lam"], out, go)      # noqa: E731
+        run = lambda: RF.backward(x, c, inp["damping"], lam, out, go)      # noqa: E731
         what = "masked reverse EMA loop + autograd through basis+einsum+tanh (oracle/reference_form.py)"
     else:
-        run = lambda: RF.forward(x, c, inp["damping"], inp["lam"])                # noqa: E731
+        run = lambda: RF.forward(x, c, inp["damping"], lam)                # noqa: E731
         what = "basis+einsum+tanh and per-head EMA loop (oracle/reference_form.py)"
-    RF.forward(x[:, :256], c, inp["damping"], inp["lam"])        # warm-up
-    times = []
-    for _ in range(2):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    t = min(times)
-    tokens = S
-    return {
+        if g is not None:
+            what += "; static lambda (the loop's cost does not depend on it)"
+    t = _median_time(run)
+    tokens = rows * S
+    res = {
         "value": tokens / t,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"one batch row of the workload: B=1 S={S} D={cfg.D} K={cfg.K} fp32, {what}, best of 2",
+        "sample": (f"{'the whole workload' if full else 'one batch row of the workload'}: B={rows} S={S} "
+                   f"D={cfg.D} K={cfg.K} fp32, {what}, median of 3 after a warm-up"),
+        "seconds": t,
         "gbs": algorithmic_bytes(cfg) / (cfg.B * cfg.S) * tokens / t / 1e9,
-        "cpu": platform.processor() or platform.machine(),
+        "cpu": cpu_model(),
         "os_cpu_count": os.cpu_count(),
     }
+    if forward_only and cfg.name != "cpu_ref":
+        # BASELINE configs[0] (B=1 S=2048 D=512), the reference's CPU-runnable case
+        c0 = CONFIGS["cpu_ref"]
+        i0 = make_config_inputs(c0)
+        t0 = _median_time(lambda: RF.forward(i0["x"], i0["coeffs"], i0["damping"], i0["lam"]))
+        res["configs0"] = {"value": c0.B * c0.S / t0, "unit": "tokens/s", "seconds": t0,
+                           "sample": "BASELINE configs[0] in full: B=1 S=2048 D=512 K=8 fp32, median of 3 after "
+                                     "a warm-up"}
+    return res
 
 
 def measured_traffic(workload: str):
@@ -119,42 +162,87 @@ def measured_traffic(workload: str):
         return None
 
 
-def _counter_rows(path: str, counter: str):
+# Kernels whose HBM traffic the summary reports (the dominant kernel of each
+# workload), and the auxiliary kernels of a step (tile merges / reductions).
+MAIN_KERNELS = ("cheby_ema_fwd_kernel", "cheby_ema_ttt_kernel", "cheby_ema_bwd_kernel", "v10_chunked_kernel")
+AUX_KERNELS = ("ttt_merge", "ttt_finalize", "bwd_reduce")
+READ_COUNTERS = ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_BUBBLE_sum")
+WRITE_COUNTERS = ("TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum")
+
+
+def _dispatch_counters(path: str):
+    """{dispatch id: (kernel name, {counter: value})} from a rocprofv3 --pmc
+    output directory (rocpd SQLite databases or counter_collection.csv)."""
     import csv
     import glob
-    files = [path] if os.path.isfile(path) else glob.glob(os.path.join(path, "**", "*counter_collection.csv"),
-                                                            recursive=True)
-    rows = []
+    import sqlite3
+    out = {}
+    files = [path] if os.path.isfile(path) else glob.glob(os.path.join(path, "**", "*"), recursive=True)
     for fn in files:
-        with open(fn) as f:
-            rows += [r for r in csv.DictReader(f) if r["Counter_Name"] == counter]
-    return sorted(rows, key=lambda r: int(r["Dispatch_Id"]))
+        if fn.endswith("_results.db"):
+            con = sqlite3.connect(fn)
+            rows = con.execute("select dispatch_id, kernel_name, counter_name, value from counters_collection")
+            for did, kn, cn, v in rows:
+                out.setdefault((fn, did), (kn, {}))[1][cn] = float(v)
+            con.close()
+        elif fn.endswith("counter_collection.csv"):
+            with open(fn) as f:
+                for r in csv.DictReader(f):
+                    key = (fn, int(r["Dispatch_Id"]))
+                    out.setdefault(key, (r["Kernel_Name"], {}))[1][r["Counter_Name"]] = float(r["Counter_Value"])
+    return dict(sorted(out.items()))
 
 
-def pmc_summary(fetch_path: str, write_path: str, workload: str) -> dict:
+def read_bytes(c: dict) -> float:
+    """HBM read bytes of one dispatch on gfx950: every TCC->EA read request
+    that is not a 32-byte one moves one 128-byte line (TCC_BUBBLE, which
+    FETCH_SIZE's formula takes as the 128-byte count, stays 0 on this chip,
+    so FETCH_SIZE counts such a request as 64 bytes).  Checked on plain
+    device copies of known size (copy_read_ratio)."""
+    r, r32 = c["TCC_EA0_RDREQ_sum"], c["TCC_EA0_RDREQ_32B_sum"]
+    return 128.0 * (r - r32) + 32.0 * r32
+
+
+def write_bytes(c: dict) -> float:
+    """HBM write bytes of one dispatch: 64-byte and 32-byte TCC->EA write
+    requests (WRITE_SIZE's formula); checked on the same copies
+    (copy_write_ratio)."""
+    w, w64 = c["TCC_EA0_WRREQ_sum"], c["TCC_EA0_WRREQ_64B_sum"]
+    return 64.0 * w64 + 32.0 * (w - w64)
+
+
+def pmc_summary(read_path: str, write_path: str, workload: str) -> dict:
     """HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc
-    runs of ``bench.py --calibrate-copy`` (FETCH_SIZE, then WRITE_SIZE, KiB
-    per dispatch).  Each counter is scaled by bytes/counter of the run's last
-    5 copy kernels (plain device copies of one x buffer, size known), then
-    stored under ``workload`` in profiles/hbm_traffic.json."""
+    runs of ``bench.py --calibrate-copy --workload W``, one with the read
+    request counters (READ_COUNTERS), one with the write ones
+    (WRITE_COUNTERS).  The run's last 5 plain device copies (one x buffer,
+    size known) validate the byte formulas: their ratios of measured to
+    known bytes are stored with the result, nothing is scaled by them.
+    Stored under ``workload`` in profiles/hbm_traffic.json."""
     cfg = CONFIGS[workload]
     copy_bytes = cfg.B * cfg.S * cfg.D * (2 if cfg.dtype == torch.bfloat16 else 4)
-    out = {}
-    for key, counter, path in (("read", "FETCH_SIZE", fetch_path), ("write", "WRITE_SIZE", write_path)):
-        rows = _counter_rows(path, counter)
-        ours = [float(r["Counter_Value"]) * 1024 for r in rows
-                if any(k in r["Kernel_Name"] for k in ("cheby_ema_fwd_kernel", "cheby_ema_ttt_kernel",
-                                                       "cheby_ema_bwd_kernel", "v10_chunked_kernel"))]
-        copies = [float(r["Counter_Value"]) * 1024 for r in rows if "copyBuffer" in r["Kernel_Name"]][-5:]
-        if not ours or len(copies) < 5:
-            raise SystemExit(f"pmc_summary: {path} lacks kernel or 5 calibration copies for {counter}")
-        scale = copy_bytes / (sum(copies) / len(copies))
-        out[f"{key}_bytes"] = scale * sum(ours) / len(ours)
-        out[f"{key}_counter_kib"] = sum(ours) / len(ours) / 1024
-        out[f"{key}_scale"] = scale
-        out[f"{key}_dispatches"] = len(ours)
+    launches = cfg.S // cfg.chunk if cfg.chunk else 1
+    out = {"method": "TCC->EA request counters: reads 128 B per non-32-byte request, writes 64/32 B per request"}
+    for key, path, fn, names in (("read", read_path, read_bytes, READ_COUNTERS),
+                                 ("write", write_path, write_bytes, WRITE_COUNTERS)):
+        disp = list(_dispatch_counters(path).values())
+        main = [fn(c) for k, c in disp if any(m in k for m in MAIN_KERNELS)]
+        aux = [fn(c) for k, c in disp if any(m in k for m in AUX_KERNELS)]
+        copies = [fn(c) for k, c in disp if "copyBuffer" in k][-5:]
+        if not main or len(copies) < 5:
+            raise SystemExit(f"pmc_summary: {path} lacks {names} for the kernel or the 5 calibration copies")
+        per = sum(main) / len(main)
+        out[f"{key}_bytes"] = per
+        out[f"{key}_dispatches"] = len(main)
+        # auxiliary kernels of a step, per launch of the main kernel
+        out[f"{key}_aux_bytes"] = sum(aux) / len(main) if aux else 0.0
+        out[f"copy_{key}_ratio"] = (sum(copies) / len(copies)) / copy_bytes
+        out[f"{key}_counters_mean"] = {n: sum(c.get(n, 0.0) for k, c in disp if any(m in k for m in MAIN_KERNELS))
+                                       / len(main) for n in names}
     out["bytes"] = out["read_bytes"] + out["write_bytes"]
-    out["algorithmic_bytes"] = algorithmic_bytes(cfg) / (cfg.S // cfg.chunk if cfg.chunk else 1)
+    out["step_bytes"] = out["bytes"] + out["read_aux_bytes"] + out["write_aux_bytes"]
+    out["algorithmic_bytes"] = algorithmic_bytes(cfg) / launches
+    out["ratio"] = out["bytes"] / out["algorithmic_bytes"]
     try:
         with open(TRAFFIC_FILE) as f:
             table = json.load(f)
@@ -182,10 +270,11 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run 5 plain device copies of one x buffer (reads and writes "
                          "B*S*D elements each) as the reference kernel for HBM counter scaling")
-    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_RUN", "WRITE_RUN"),
-                    help="no GPU work: turn two rocprofv3 --pmc outputs (FETCH_SIZE, WRITE_SIZE) of "
-                         "'bench.py --calibrate-copy --workload W' into HBM bytes per launch for W, "
-                         "stored in profiles/hbm_traffic.json")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("READ_RUN", "WRITE_RUN"),
+                    help="no GPU work: turn two rocprofv3 --pmc outputs of 'bench.py --calibrate-copy "
+                         "--workload W' (read request counters, then write request counters; see "
+                         "READ_COUNTERS / WRITE_COUNTERS) into HBM bytes per launch for W, stored in "
+                         "profiles/hbm_traffic.json")
     args = ap.parse_args()
     if args.pmc_summary:
         print(json.dumps({args.workload: pmc_summary(*args.pmc_summary, args.workload)}, indent=1))
