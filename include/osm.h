@@ -4,7 +4,7 @@
  * One fused operator, per batch b, token t, head h, lane j (d = h*hd + j):
  *
  *   u = x / (1 + |x|)                               softsign
- *   p = sum_{k<K} c[b,h,k,j] T_k(u)                 Clenshaw, K <= 8
+ *   p = sum_{k<K} c[b,h,k,j] T_k(u)                 Clenshaw, K <= 16 (<= 8 for the TTT)
  *   z = tanh(damping[h] * p)                        (z = 0 where x is NaN, or u = 0
  *                                                    with OSM_FLAG_NAN_ZERO_U)
  *   s[t] = lam[b,t,h] s[t-1] + (1 - lam[b,t,h]) z   s[-1] = ema_init (0 if NULL)
@@ -73,7 +73,8 @@ extern "C" {
 #endif
 
 #define OSM_ABI_VERSION 2
-#define OSM_MAX_K 8
+#define OSM_MAX_K 16      /* coefficients per lane: forward and backward */
+#define OSM_MAX_K_TTT 8   /* coefficients per lane: the TTT gradient */
 
 typedef enum osm_dtype { OSM_F32 = 0, OSM_BF16 = 1 } osm_dtype;
 
@@ -102,14 +103,17 @@ typedef enum osm_ttt_target { OSM_TARGET_X = 0, OSM_TARGET_SOFTSIGN = 1 } osm_tt
 
 /*
  * Operator arguments.  Strides are in elements.  The lane (last) dimension of
- * x, out and coeffs is contiguous.  x and out rows start on 4-element
- * boundaries: pointer aligned to 4 elements, x_stride_b/x_stride_s (and the
- * out strides) multiples of 4.
+ * x, out and coeffs is contiguous; pointers are aligned to their element
+ * size and strides are non-negative.  The forward is fastest when hd % 4 == 0,
+ * K <= 8 and the x and out rows start on 4-element boundaries (pointers
+ * aligned to 4 elements, x_stride_b/x_stride_s and the out strides multiples
+ * of 4); other layouts take a one-lane-per-thread geometry, and K > 8 the
+ * Clenshaw form of the series.
  */
 typedef struct osm_cheby_args {
   int32_t abi_version;      /* = OSM_ABI_VERSION */
   int32_t flags;            /* OSM_FLAG_* */
-  int64_t B, S, H, hd, K;   /* hd % 4 == 0, 1 <= K <= 8 */
+  int64_t B, S, H, hd, K;   /* hd >= 1, 1 <= K <= OSM_MAX_K (OSM_MAX_K_TTT for the TTT) */
 
   const void* x;            /* [B,S,H*hd] of x_dtype */
   int32_t x_dtype;
@@ -229,7 +233,8 @@ const char* osm_last_error(void);
 
 /* Workspace bytes needed by osm_cheby_ema_fwd (op = OSM_OP_FWD),
  * osm_cheby_ema_ttt (OSM_OP_TTT) or osm_cheby_ema_bwd (OSM_OP_BWD).  Reads
- * only the shape fields, dtypes, K and whether g is NULL; returns 0 if those
+ * only the shape fields, dtypes, K, whether g is NULL and (forward) the x/out
+ * strides and pointer alignment that choose its geometry; returns 0 if those
  * are invalid. */
 size_t osm_workspace_bytes(const osm_cheby_args* args, int op);
 

@@ -43,15 +43,22 @@ struct Geometry {
   int n_lbd = 0, n_lb = 0, n_lb_pad = 0, n_tiles = 0;
   int tile = 0;        // tokens per tile
   int lanes = 64;      // lanes per lane-block
+  int lpt = 2;         // lanes per thread (forward)
   bool dyn = false;
   int kpad = 8;
   bool empty = false;  // B == 0 or S == 0
 };
 
 bool aligned4(const void* p, int esize) { return ((uintptr_t)p % (uintptr_t)(4 * esize)) == 0; }
+bool aligned1(const void* p, int esize) { return ((uintptr_t)p % (uintptr_t)esize) == 0; }
 
 // Validates `a` without touching the GPU and fills `geo` for the entry point
 // `op` (an osm_op; the forward's tile shape comes from osm::fwd_geometry).
+// The forward's two-lane geometries need hd % 4 == 0, x/out rows on
+// 4-element boundaries and K <= 8; any other layout, and K up to
+// OSM_MAX_K, takes its one-lane geometry.  The backward and the TTT hold
+// one lane per thread and need rows aligned to one element; the TTT takes
+// K <= OSM_MAX_K_TTT.
 int check_args(const osm_cheby_args* a, Geometry* geo, int op, bool shapes_only = false) {
   if (!a) return fail(OSM_E_ARG, "args is NULL");
   if (a->abi_version != OSM_ABI_VERSION)
@@ -59,32 +66,35 @@ int check_args(const osm_cheby_args* a, Geometry* geo, int op, bool shapes_only 
   const int known = OSM_FLAG_NO_CLAMP | OSM_FLAG_NAN_ZERO_U | (op == OSM_OP_BWD ? OSM_FLAG_FULL_JACOBIAN : 0);
   if (a->flags & ~known) return fail(OSM_E_ARG, "unknown flag bits 0x%x", a->flags);
   if (a->B < 0 || a->S < 0) return fail(OSM_E_SHAPE, "B=%lld and S=%lld must be >= 0", (long long)a->B, (long long)a->S);
-  if (a->H < 1 || a->hd < 4 || a->hd % 4 != 0)
-    return fail(OSM_E_SHAPE, "need H >= 1 and hd a positive multiple of 4 (H=%lld hd=%lld)", (long long)a->H,
-                (long long)a->hd);
-  if (a->K < 1 || a->K > OSM_MAX_K) return fail(OSM_E_SHAPE, "K=%lld outside [1, %d]", (long long)a->K, OSM_MAX_K);
+  if (a->H < 1 || a->hd < 1)
+    return fail(OSM_E_SHAPE, "need H >= 1 and hd >= 1 (H=%lld hd=%lld)", (long long)a->H, (long long)a->hd);
+  const int max_k = op == OSM_OP_TTT ? OSM_MAX_K_TTT : OSM_MAX_K;
+  if (a->K < 1 || a->K > max_k)
+    return fail(OSM_E_SHAPE, "K=%lld outside [1, %d]%s", (long long)a->K, max_k,
+                op == OSM_OP_TTT ? " (the TTT gradient)" : "");
   const int64_t D = a->H * a->hd;
   if (D > (int64_t(1) << 28)) return fail(OSM_E_SHAPE, "D=H*hd=%lld too large", (long long)D);
   if (a->x_dtype != OSM_F32 && a->x_dtype != OSM_BF16) return fail(OSM_E_DTYPE, "x_dtype %d unsupported", a->x_dtype);
   if (a->out_dtype != OSM_F32 && a->out_dtype != OSM_BF16)
     return fail(OSM_E_DTYPE, "out_dtype %d unsupported", a->out_dtype);
   geo->dyn = a->g != nullptr;
-  geo->kpad = a->K <= 4 ? 4 : 8;
+  geo->kpad = a->K <= 4 ? 4 : (a->K <= 8 ? 8 : 16);
   geo->empty = a->B == 0 || a->S == 0;
+  const int xs = a->x_dtype == OSM_F32 ? 4 : 2;
+  const int os = a->out_dtype == OSM_F32 ? 4 : 2;
+  const bool rows4 = a->hd % 4 == 0 && aligned4(a->x, xs) && a->x_stride_b % 4 == 0 && a->x_stride_s % 4 == 0 &&
+                     aligned4(a->out, os) && a->out_stride_b % 4 == 0 && a->out_stride_s % 4 == 0;
+  const bool generic = op == OSM_OP_FWD && (!rows4 || a->K > osm::kMonoMaxK);
   if (geo->empty) return OSM_OK;
   // The backward reads out only for the clamp mask.
   const bool need_out = op != OSM_OP_BWD || !(a->flags & OSM_FLAG_NO_CLAMP);
   if (!shapes_only) {
     if (!a->x || (need_out && !a->out) || !a->coeffs || !a->damping || !a->lam)
       return fail(OSM_E_ARG, "x, out, coeffs, damping and lam must be non-NULL");
-    const int xs = a->x_dtype == OSM_F32 ? 4 : 2;
-    const int os = a->out_dtype == OSM_F32 ? 4 : 2;
-    if (!aligned4(a->x, xs) || a->x_stride_b % 4 || a->x_stride_s % 4 || a->x_stride_b < 0 || a->x_stride_s < 0)
-      return fail(OSM_E_LAYOUT, "x must be aligned to 4 elements with non-negative strides that are multiples of 4");
-    if (a->out && (!aligned4(a->out, os) || a->out_stride_b % 4 || a->out_stride_s % 4 || a->out_stride_b < 0 ||
-                   a->out_stride_s < 0))
-      return fail(OSM_E_LAYOUT,
-                  "out must be aligned to 4 elements with non-negative strides that are multiples of 4");
+    if (!aligned1(a->x, xs) || a->x_stride_b < 0 || a->x_stride_s < 0)
+      return fail(OSM_E_LAYOUT, "x must be element-aligned with non-negative strides");
+    if (a->out && (!aligned1(a->out, os) || a->out_stride_b < 0 || a->out_stride_s < 0))
+      return fail(OSM_E_LAYOUT, "out must be element-aligned with non-negative strides");
     if (geo->dyn && !(a->lam_min <= a->lam_max))
       return fail(OSM_E_ARG, "lam_min %g > lam_max %g", (double)a->lam_min, (double)a->lam_max);
     // Rows of out must not overlap (padding rows of the last tile are masked
@@ -107,9 +117,9 @@ int check_args(const osm_cheby_args* a, Geometry* geo, int op, bool shapes_only 
         a->c_stride_k < 0 || a->c_stride_b < 0)
       return fail(OSM_E_LAYOUT, "coeffs strides must be non-negative and fit 31-bit offsets");
   }
-  osm::FwdShape shape{osm::ttt_tile_tokens(geo->dyn, a->x_dtype), osm::TttTile::LANES};
-  if (op == OSM_OP_FWD) shape = osm::fwd_geometry(geo->dyn, a->B, D, a->S);
-  if (op == OSM_OP_BWD) shape = osm::FwdShape{osm::bwd_tile_tokens(geo->dyn), osm::BwdTile::LANES};
+  osm::FwdShape shape{osm::ttt_tile_tokens(geo->dyn, a->x_dtype), osm::TttTile::LANES, 1};
+  if (op == OSM_OP_FWD) shape = osm::fwd_geometry(geo->dyn, a->B, D, a->S, generic);
+  if (op == OSM_OP_BWD) shape = osm::FwdShape{osm::bwd_tile_tokens(geo->dyn, geo->kpad), osm::BwdTile::LANES, 1};
   const int64_t tile = shape.tile;
   const int64_t n_lbd = (D + shape.lanes - 1) / shape.lanes;
   const int64_t n_lb = a->B * n_lbd;
@@ -123,6 +133,7 @@ int check_args(const osm_cheby_args* a, Geometry* geo, int op, bool shapes_only 
   geo->n_tiles = (int)n_tiles;
   geo->tile = (int)tile;
   geo->lanes = shape.lanes;
+  geo->lpt = shape.lpt;
   return OSM_OK;
 }
 
@@ -197,20 +208,20 @@ int hip_fail(hipError_t e, const char* what) {
 // workspace seen for the first time is cleared in full (header included),
 // unless osm_workspace_init zeroed it.
 struct Layout {
-  int n_lb, n_tiles, tile, lanes, kpad;
+  int n_lb, n_tiles, tile, lanes, lpt, kpad;
   bool dyn;
   int op;
   bool operator==(const Layout& o) const {
-    return n_lb == o.n_lb && n_tiles == o.n_tiles && tile == o.tile && lanes == o.lanes && kpad == o.kpad &&
-           dyn == o.dyn && op == o.op;
+    return n_lb == o.n_lb && n_tiles == o.n_tiles && tile == o.tile && lanes == o.lanes && lpt == o.lpt &&
+           kpad == o.kpad && dyn == o.dyn && op == o.op;
   }
 };
-const Layout kZeroed{-1, -1, -1, -1, -1, false, -1};
+const Layout kZeroed{-1, -1, -1, -1, -1, -1, false, -1};
 std::mutex g_ws_mu;
 std::unordered_map<uintptr_t, Layout> g_ws_layout;
 
 int prepare_workspace(void* ws, size_t need, const Geometry& geo, int op, hipStream_t stream) {
-  const Layout now{geo.n_lb, geo.n_tiles, geo.tile, geo.lanes, geo.kpad, geo.dyn, op};
+  const Layout now{geo.n_lb, geo.n_tiles, geo.tile, geo.lanes, geo.lpt, geo.kpad, geo.dyn, op};
   bool fresh, clear;
   {
     std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -335,7 +346,7 @@ int osm_cheby_ema_fwd(const osm_cheby_args* args, void* workspace, size_t worksp
                          OSM_OP_FWD, st);
   if (rc != OSM_OK) return rc;
   const osm::FwdParams p = make_params(args, geo, workspace);
-  const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, osm::FwdShape{geo.tile, geo.lanes}, geo.kpad, st);
+  const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, osm::FwdShape{geo.tile, geo.lanes, geo.lpt}, geo.kpad, st);
   if (e != hipSuccess) return hip_fail(e, "forward kernel launch");
   return ok();
 }
@@ -356,7 +367,7 @@ int osm_cheby_ema_fwd_static(const osm_cheby_args* args, void* stream) {
   void* ws;
   rc = static_scratch_ptr(&dev, &ws);
   if (rc != OSM_OK) return rc;
-  const Layout now{geo.n_lb, geo.n_tiles, geo.tile, geo.lanes, geo.kpad, geo.dyn, OSM_OP_FWD};
+  const Layout now{geo.n_lb, geo.n_tiles, geo.tile, geo.lanes, geo.lpt, geo.kpad, geo.dyn, OSM_OP_FWD};
   size_t skip = 0;
   bool clear;
   {
@@ -376,7 +387,7 @@ int osm_cheby_ema_fwd_static(const osm_cheby_args* args, void* stream) {
     }
   }
   const osm::FwdParams p = make_params(args, geo, ws);
-  const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, osm::FwdShape{geo.tile, geo.lanes},
+  const hipError_t e = osm::launch_fwd(p, args->x_dtype, args->out_dtype, geo.dyn, osm::FwdShape{geo.tile, geo.lanes, geo.lpt},
                                        geo.kpad, st);
   if (e != hipSuccess) return hip_fail(e, "forward kernel launch");
   return ok();
@@ -423,7 +434,10 @@ int osm_v10_chunked_ttt(const osm_v10_args* a, void* stream) {
   if (a->B < 0 || a->S < 0 || a->H < 1 || a->hd < 1)
     return fail(OSM_E_SHAPE, "need B, S >= 0, H, hd >= 1 (B=%lld S=%lld H=%lld hd=%lld)", (long long)a->B,
                 (long long)a->S, (long long)a->H, (long long)a->hd);
-  if (a->K < 1 || a->K > OSM_MAX_K) return fail(OSM_E_SHAPE, "K=%lld outside [1, %d]", (long long)a->K, OSM_MAX_K);
+  // The reference's kernels clamp the degree to 8 (sdpc_kernel.py:2379);
+  // callers pass coefficients past the eighth around the full path.
+  constexpr int kMaxKV10 = 8;
+  if (a->K < 1 || a->K > kMaxKV10) return fail(OSM_E_SHAPE, "K=%lld outside [1, %d]", (long long)a->K, kMaxKV10);
   if (a->chunk < 1) return fail(OSM_E_SHAPE, "chunk=%lld must be >= 1", (long long)a->chunk);
   if (a->x_dtype != OSM_F32 && a->x_dtype != OSM_BF16) return fail(OSM_E_DTYPE, "x_dtype %d unsupported", a->x_dtype);
   const int64_t D = a->H * a->hd;
@@ -529,12 +543,10 @@ int osm_cheby_ema_bwd(const osm_cheby_args* args, const osm_cheby_bwd_args* bwd,
   if (!bwd->grad_out || !bwd->grad_x) return fail(OSM_E_ARG, "grad_out and grad_x must be non-NULL");
   const int xs = args->x_dtype == OSM_F32 ? 4 : 2;
   const int os = args->out_dtype == OSM_F32 ? 4 : 2;
-  if (!aligned4(bwd->grad_out, os) || bwd->go_stride_b % 4 || bwd->go_stride_s % 4 || bwd->go_stride_b < 0 ||
-      bwd->go_stride_s < 0)
-    return fail(OSM_E_LAYOUT,
-                "grad_out must be aligned to 4 elements with non-negative strides that are multiples of 4");
-  if (!aligned4(bwd->grad_x, xs) || bwd->gx_stride_b % 4 || bwd->gx_stride_s % 4)
-    return fail(OSM_E_LAYOUT, "grad_x must be aligned to 4 elements with strides that are multiples of 4");
+  if (!aligned1(bwd->grad_out, os) || bwd->go_stride_b < 0 || bwd->go_stride_s < 0)
+    return fail(OSM_E_LAYOUT, "grad_out must be element-aligned with non-negative strides");
+  if (!aligned1(bwd->grad_x, xs))
+    return fail(OSM_E_LAYOUT, "grad_x must be element-aligned");
   if (bwd->gx_stride_s < D || bwd->gx_stride_b < args->S * bwd->gx_stride_s)
     return fail(OSM_E_LAYOUT, "grad_x rows/batches overlap (gx_stride_s=%lld < D or gx_stride_b too small)",
                 (long long)bwd->gx_stride_s);

@@ -88,8 +88,10 @@ __device__ __forceinline__ void accumulate_basis(float (&Gk)[KP], float e, float
 }
 
 // Pass 2 over a thread's run, last token first, from v = v[t_end + 1].
-// c: the lane's scaled monomial coefficients (y = sum c_j u^j); dm: those of
-// y' times 2 ln2 (and 1 - lam for a static lambda).  SLOW handles, per
+// c: the lane's scaled series coefficients (monomial, y = sum c_j u^j, or
+// Chebyshev, y = sum c_k T_k(u), for more than kMonoMaxK of them; see
+// series()); dm[m] = (m+1) c[m+1] times 2 ln2 (and 1 - lam for a static
+// lambda): y' = sum dm[m] u^m, or sum dm[m] U_m(u) in the Chebyshev form.  SLOW handles, per
 // element, tokens >= S (r >= n_valid: identity map, no contribution), the clamp mask
 // (mbits bit r set: m = 0), NaN inputs (u = 0; e = 0 unless nan_zero_u);
 // the fast variant assumes none of them occurs in the run.  ZS: 1 - z^2 comes
@@ -124,14 +126,17 @@ __device__ __forceinline__ void bwd_pass2(float& v, float (&Gk)[KP], const float
     if constexpr (ZS) {
       hq = 0.25f * __builtin_fmaf(-zv[r], zv[r], 1.0f);
     } else {
-      const float rr = tanh_r(horner<KP>(u, c));
+      const float rr = tanh_r(series<KP>(u, c));
       hq = __builtin_fmaf(-rr, rr, rr);
     }
     float e = av * hq;
     if constexpr (DYN) e *= 1.0f - lam;
     if constexpr (SLOW) e = live ? e : 0.0f;
     float dy = 0.0f;
-    if constexpr (KP > 1) dy = horner<KP - 1>(u, dm);
+    if constexpr (KP > kMonoMaxK)
+      dy = clenshaw_u<KP - 1>(u, dm);
+    else if constexpr (KP > 1)
+      dy = horner<KP - 1>(u, dm);
     float gxv[1] = {e * dy * ir * ir};
     if (!full_jac) gxv[0] = __builtin_fabsf(x) >= kSoftsignGradMin ? gxv[0] : 0.0f;
     BufVec<XT, 1>::store(gx.r, gx.v, so, gxv);
@@ -379,6 +384,13 @@ hipError_t launch_all(const BwdParams& bp, hipStream_t stream) {
 
 template <bool DYN, typename XT, typename OT>
 hipError_t launch_k(const BwdParams& bp, int tile, int kpad, hipStream_t stream) {
+  if (kpad == 16) {
+    // Chebyshev form: shorter runs leave room for 3 x 16 coefficient and
+    // gradient registers.
+    if (tile != BwdTileCheb::TILE) return hipErrorInvalidValue;
+    if (bp.zs) return hipErrorInvalidValue;
+    return launch_all<BwdTileCheb, DYN, false, XT, OT, 16>(bp, stream);
+  }
   using G = BwdTile;
   if (tile != G::TILE) return hipErrorInvalidValue;
   if (bp.zs) {
@@ -403,12 +415,12 @@ hipError_t launch_dt(const BwdParams& bp, int x_dtype, int out_dtype, int tile, 
 
 }  // namespace
 
-int bwd_tile_tokens(bool) { return BwdTile::TILE; }
+int bwd_tile_tokens(bool, int kpad) { return kpad > kMonoMaxK ? BwdTileCheb::TILE : BwdTile::TILE; }
 
 size_t bwd_slot_bytes(int n_lb, int n_tiles) { return fwd_workspace_bytes(n_lb, n_tiles, kLanes, true); }
 
 size_t bwd_workspace_bytes(int n_lb, int n_tiles, int K) {
-  const size_t kpad = K <= 4 ? 4 : 8;
+  const size_t kpad = K <= 4 ? 4 : (K <= 8 ? 8 : 16);
   const size_t slots = (bwd_slot_bytes(n_lb, n_tiles) + 255) / 256 * 256;
   return slots + (size_t)n_lb * n_tiles * kpad * kLanes * sizeof(float);
 }

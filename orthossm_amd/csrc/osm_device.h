@@ -347,6 +347,35 @@ __device__ __forceinline__ float horner(float u, const float (&a)[KP]) {
   return p;
 }
 
+// The series of a lane from the coefficients the kernels hold in registers:
+// monomial coefficients (Horner) for KP <= kMonoMaxK, Chebyshev coefficients
+// (Clenshaw) above.
+template <int KP>
+__device__ __forceinline__ float series(float u, const float (&c)[KP]) {
+  if constexpr (KP > kMonoMaxK)
+    return clenshaw<KP>(u, c);
+  else
+    return horner<KP>(u, c);
+}
+
+// Clenshaw evaluation of sum_{m<N} d[m] U_m(u) in the second-kind basis
+// (U_0 = 1, U_1 = 2u, U_m = 2u U_{m-1} - U_{m-2}):
+//   b_m = d_m + 2u b_{m+1} - b_{m+2},  sum = b_0.
+// With d[m] = (m+1) c[m+1] it is the derivative of sum_k c_k T_k(u), since
+// T_k' = k U_{k-1}.
+template <int N>
+__device__ __forceinline__ float clenshaw_u(float u, const float (&d)[N]) {
+  const float u2 = u + u;
+  float b1 = 0.0f, b2 = 0.0f;
+#pragma unroll
+  for (int m = N - 1; m >= 0; --m) {
+    const float b0 = __builtin_fmaf(u2, b1, d[m] - b2);
+    b2 = b1;
+    b1 = b0;
+  }
+  return b1;
+}
+
 // Given y2 = 2*log2(e) * damping * p, returns r = 1 / (1 + exp(2*damping*p));
 // then tanh(damping*p) = 1 - 2r.  exp2 overflow to +Inf gives r = 0 (z = 1);
 // underflow to 0 gives r = 1 (z = -1).

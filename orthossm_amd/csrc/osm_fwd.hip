@@ -28,7 +28,7 @@ template <int KP>
 __device__ __forceinline__ float ema_input_exact(float x, const float (&a)[KP], float one_m, float neg2_one_m,
                                                  bool nan_zero_u) {
   const bool ok = x == x;
-  const float r = tanh_r(horner<KP>(ok ? softsign(x) : 0.0f, a));
+  const float r = tanh_r(series<KP>(ok ? softsign(x) : 0.0f, a));
   const float w = __builtin_fmaf(neg2_one_m, r, one_m);
   return (ok || nan_zero_u) ? w : 0.0f;
 }
@@ -168,12 +168,20 @@ cheby_ema_fwd_kernel(const FwdParams p) {
         py[rr][i] = c[i][KP - 1];
       }
     }
-#pragma unroll
-    for (int j = KP - 2; j >= 0; --j)
+    if constexpr (KP > kMonoMaxK) {
+      // Chebyshev form (more than kMonoMaxK terms): Clenshaw per element.
 #pragma unroll
       for (int rr = 0; rr < kRB; ++rr)
 #pragma unroll
-        for (int i = 0; i < LPT; ++i) py[rr][i] = __builtin_fmaf(py[rr][i], u[rr][i], c[i][j]);
+        for (int i = 0; i < LPT; ++i) py[rr][i] = series<KP>(u[rr][i], c[i]);
+    } else {
+#pragma unroll
+      for (int j = KP - 2; j >= 0; --j)
+#pragma unroll
+        for (int rr = 0; rr < kRB; ++rr)
+#pragma unroll
+          for (int i = 0; i < LPT; ++i) py[rr][i] = __builtin_fmaf(py[rr][i], u[rr][i], c[i][j]);
+    }
 #pragma unroll
     for (int rr = 0; rr < kRB; ++rr) {
       const float lam = lamv[r0 + rr];
@@ -231,18 +239,36 @@ hipError_t launch_g(const FwdParams& p, int kpad, hipStream_t stream) {
   const unsigned grid = (unsigned)p.n_lb_pad * (unsigned)p.n_tiles;
   if (kpad == 4)
     hipLaunchKernelGGL((cheby_ema_fwd_kernel<G, DYN, XT, OT, 4>), dim3(grid), dim3(G::THREADS), 0, stream, p);
-  else
+  else if (kpad == 8)
     hipLaunchKernelGGL((cheby_ema_fwd_kernel<G, DYN, XT, OT, 8>), dim3(grid), dim3(G::THREADS), 0, stream, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// The one-lane geometry also serves the Chebyshev form (kpad 16); K <= 4
+// runs with kpad 8 there (zero coefficients), one instantiation fewer.
+template <bool DYN, typename XT, typename OT>
+hipError_t launch_generic(const FwdParams& p, int kpad, hipStream_t stream) {
+  using G = FwdTileGeneric;
+  const unsigned grid = (unsigned)p.n_lb_pad * (unsigned)p.n_tiles;
+  if (kpad <= 8)
+    hipLaunchKernelGGL((cheby_ema_fwd_kernel<G, DYN, XT, OT, 8>), dim3(grid), dim3(G::THREADS), 0, stream, p);
+  else if (kpad == 16)
+    hipLaunchKernelGGL((cheby_ema_fwd_kernel<G, DYN, XT, OT, 16>), dim3(grid), dim3(G::THREADS), 0, stream, p);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
 template <class G>
 bool is_shape(FwdShape s) {
-  return s.tile == G::TILE && s.lanes == G::LANES;
+  return s.tile == G::TILE && s.lanes == G::LANES && s.lpt == G::LPT;
 }
 
 template <bool DYN, typename XT, typename OT>
 hipError_t launch_k(const FwdParams& p, FwdShape s, int kpad, hipStream_t stream) {
+  if (is_shape<FwdTileGeneric>(s)) return launch_generic<DYN, XT, OT>(p, kpad, stream);
   if constexpr (!DYN) {
     if (is_shape<FwdTileLarge>(s)) return launch_g<FwdTileLarge, DYN, XT, OT>(p, kpad, stream);
   }
@@ -285,17 +311,18 @@ __global__ void copy_state_kernel(const float* src, float* dst, size_t n) {
 
 }  // namespace
 
-FwdShape fwd_geometry(bool dyn, int64_t B, int64_t D, int64_t S) {
+FwdShape fwd_geometry(bool dyn, int64_t B, int64_t D, int64_t S, bool generic) {
+  if (generic) return {FwdTileGeneric::TILE, FwdTileGeneric::LANES, FwdTileGeneric::LPT};
   // The largest tile that still leaves >= kMinTiles workgroups with work (2
   // per CU on a 256-CU MI355X, the residency of the large tile); dynamic
   // lambda holds more per-token state and is limited to the medium tile.
   constexpr int64_t kMinTiles = 512;
   auto n_work = [&](int tile, int lanes) { return B * ((D + lanes - 1) / lanes) * ((S + tile - 1) / tile); };
   if (!dyn && n_work(FwdTileLarge::TILE, FwdTileLarge::LANES) >= kMinTiles)
-    return {FwdTileLarge::TILE, FwdTileLarge::LANES};
+    return {FwdTileLarge::TILE, FwdTileLarge::LANES, FwdTileLarge::LPT};
   if (n_work(FwdTileMedium::TILE, FwdTileMedium::LANES) >= kMinTiles)
-    return {FwdTileMedium::TILE, FwdTileMedium::LANES};
-  return {FwdTileSmall::TILE, FwdTileSmall::LANES};
+    return {FwdTileMedium::TILE, FwdTileMedium::LANES, FwdTileMedium::LPT};
+  return {FwdTileSmall::TILE, FwdTileSmall::LANES, FwdTileSmall::LPT};
 }
 
 size_t slot_words(bool dyn) { return dyn ? 2 : 1; }

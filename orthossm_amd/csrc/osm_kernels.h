@@ -10,6 +10,11 @@
 
 namespace osm {
 
+// Largest padded coefficient count evaluated in monomial form.  Beyond it
+// the monomial coefficients of T_k grow like 2^(k-1) and cancel in fp32, so
+// longer series keep their Chebyshev coefficients and use Clenshaw.
+constexpr int kMonoMaxK = 8;
+
 // Tile geometry.  A lane-block is LANES (64 or 128) consecutive lanes of one
 // batch row; a tile is TILE consecutive tokens of a lane-block and is one
 // workgroup.  A thread owns LPT adjacent lanes and a run of R consecutive
@@ -52,14 +57,22 @@ struct TileGeo {
 using FwdTileLarge = TileGeo<2, 8, 32>;           // 512 tokens x 64 lanes
 using FwdTileMedium = TileGeo<2, 8, 16, 64, 1>;   // 256 tokens x 64 lanes
 using FwdTileSmall = TileGeo<2, 8, 8, 64, 1>;     // 128 tokens x 64 lanes
+// One lane per thread: any head size, rows aligned to one element, and the
+// Chebyshev form of longer series (more than kMonoMaxK coefficients), whose
+// coefficients take twice the registers.  Used only where the geometries
+// above do not apply.
+using FwdTileGeneric = TileGeo<1, 8, 16, 64, 1>;  // 128 tokens x 64 lanes
 constexpr int kMaxTileRows = 512;              // bound on TILE (+1 row read past a tile)
 
 // Geometry of a forward launch.
 struct FwdShape {
   int tile;    // tokens per tile
   int lanes;   // lanes per lane-block
+  int lpt;     // lanes per thread
 };
-FwdShape fwd_geometry(bool dyn, int64_t B, int64_t D, int64_t S);
+// `generic`: the one-lane geometry (head size not a multiple of 4, rows not
+// on 4-element boundaries, or more than 8 coefficients).
+FwdShape fwd_geometry(bool dyn, int64_t B, int64_t D, int64_t S, bool generic);
 
 // TTT: keeps the raw x and r = 1/(1+exp(2 damping p)) of every token of the
 // run in registers, plus 2K gradient accumulators per lane: one lane per
@@ -89,7 +102,9 @@ int ttt_tile_tokens(bool dyn, int x_dtype);
 // tokens 114.3, 28 tokens 118.2, 32 tokens 114.2; 8-token runs are slower
 // (185 us).
 using BwdTile = TileGeo<1, 8, 24, 64, 2>;   // 192 tokens
-int bwd_tile_tokens(bool dyn);
+// More than 8 coefficients (Chebyshev form, kpad 16): 12-token runs.
+using BwdTileCheb = TileGeo<1, 8, 12, 64, 2>;   // 96 tokens
+int bwd_tile_tokens(bool dyn, int kpad);
 
 // Workspace: a kHeaderBytes header (launch epoch, fault word, completion
 // counters), then the look-back words, then (TTT and backward) per-tile

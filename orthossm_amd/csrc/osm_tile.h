@@ -60,11 +60,14 @@ __device__ __forceinline__ uint32_t next_off(uint32_t off, uint32_t step) {
   return off;
 }
 
-// Monomial coefficients of the series for the tile's lanes, scaled by
-// 2*log2(e)*damping (the tanh argument in exp2 units).  The work is split in
-// units (coefficient j, 64-lane sub-block sb); wave w takes units w, w +
-// WAVES, ... and forms coefficient j of its 64 lanes from <= 4 Chebyshev
-// coefficients (kChebMono) in float64; results are shared through LDS.
+// Coefficients of the series for the tile's lanes, scaled by
+// 2*log2(e)*damping (the tanh argument in exp2 units): the monomial form for
+// KP <= kMonoMaxK, the Chebyshev coefficients themselves above (evaluated by
+// Clenshaw, see series()).  The work is split in units (coefficient j,
+// 64-lane sub-block sb); wave w takes units w, w + WAVES, ... and forms
+// coefficient j of its 64 lanes from <= 4 Chebyshev coefficients
+// (kChebMono) in float64 (monomial form) or scales c_j (Chebyshev form);
+// results are shared through LDS.
 // Split in three steps so the caller can issue these loads before its bulk
 // loads (the conversion then waits only for them) and convert after issuing
 // those:
@@ -74,7 +77,8 @@ template <int KP, class G>
 struct MonoLoad {
   static constexpr int NU = KP * G::NSUB;                   // units
   static constexpr int NJ = (NU + G::WAVES - 1) / G::WAVES;  // units per wave
-  float cm[NJ][4];
+  static constexpr int NT = KP > kMonoMaxK ? 1 : 4;          // coefficients read per unit
+  float cm[NJ][NT];
   float kap[NJ];
   int w;   // wave index (wave-uniform)
 };
@@ -93,7 +97,7 @@ __device__ __forceinline__ MonoLoad<KP, G> mono_issue(const FwdParams& p, const 
     const int h = ok ? div_hd(d, p) : 0;
     const uint32_t vc = ok ? (uint32_t)(((int64_t)h * p.c_sh + (d - h * p.hd)) * 4) : kOffOOB;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < m.NT; ++i) {
       // Unconditional loads (an unused unit or k >= K reads 0 through the
       // out-of-range offset): a branch here would make the compiler convert
       // each value inside it and so wait for every load on the spot, before
@@ -117,8 +121,12 @@ __device__ __forceinline__ void mono_store(const MonoLoad<KP, G>& m, const Threa
     if (u < m.NU) {
       const int j = u / G::NSUB;
       double acc = 0.0;
+      if constexpr (KP > kMonoMaxK) {
+        acc = (double)m.cm[n][0];
+      } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc = __builtin_fma((double)kChebMono[j][i], (double)m.cm[n][i], acc);
+        for (int i = 0; i < 4; ++i) acc = __builtin_fma((double)kChebMono[j][i], (double)m.cm[n][i], acc);
+      }
       mono[j][(u % G::NSUB) * kLanes + q.wl] = (float)(acc * (double)m.kap[n]);
     }
   }

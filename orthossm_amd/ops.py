@@ -121,7 +121,7 @@ def _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, 
     dev = x.device
     if x.dtype not in (torch.float32, torch.bfloat16):
         x = x.float()
-    if x.stride(2) != 1 or x.stride(1) % 4 or x.stride(0) % 4 or x.data_ptr() % (4 * x.element_size()):
+    if x.stride(2) != 1 or min(x.stride()) < 0:
         x = x.contiguous()
     B, S, D = x.shape
     if coeffs.dim() != 4:
@@ -150,9 +150,8 @@ def _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, 
             out = torch.empty((B, S, D), device=dev, dtype=odt)
     elif tuple(out.shape) != (B, S, D) or out.dtype != odt or out.device != dev:
         raise ValueError("out has the wrong shape, dtype or device")
-    if out is not None and (out.stride(2) != 1 or out.stride(1) % 4 or out.stride(0) % 4
-                            or out.data_ptr() % (4 * out.element_size())):
-        raise ValueError("out must have a contiguous lane dimension and 4-element aligned rows")
+    if out is not None and (out.stride(2) != 1 or min(out.stride()) < 0):
+        raise ValueError("out must have a contiguous lane dimension and non-negative strides")
     a = nat.ChebyArgs()
     a.abi_version = nat.ABI_VERSION
     if nan_policy not in ("zero_z", "zero_u"):
@@ -277,7 +276,7 @@ def cheby_ema_backward(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, out:
     go = grad_out.to(device=dev, dtype=out_dt)
     if tuple(go.shape) != (B, S, D):
         raise ValueError(f"grad_out must be [B,S,D]=({B},{S},{D}), got {tuple(grad_out.shape)}")
-    if go.stride(2) != 1 or go.stride(1) % 4 or go.stride(0) % 4 or go.data_ptr() % (4 * go.element_size()):
+    if go.stride(2) != 1 or min(go.stride()) < 0:
         go = go.contiguous()
     if grad_x_out is None:
         gx = torch.empty((B, S, D), device=dev, dtype=xin.dtype)
@@ -473,7 +472,7 @@ def v10_chunked_ttt(x: torch.Tensor, coeffs: torch.Tensor, momentum: torch.Tenso
             c_full.shape[1] * c_full.shape[3] != D or m_full.shape != c_full.shape:
         raise ValueError(f"coeffs/momentum must be [B,H,K,hd] matching x {tuple(x.shape)} and n_heads={n_heads}")
     H, Kfull, hd = n_heads, c_full.shape[2], c_full.shape[3]
-    K = min(Kfull, nat.MAX_K)
+    K = min(Kfull, nat.MAX_K_V10)
     c = c_full[:, :, :K]
     m = m_full[:, :, :K]
     if c.stride(3) != 1:

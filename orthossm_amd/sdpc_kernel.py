@@ -52,6 +52,8 @@ LUT_TABLE_SIZE: int = LUT_POINTS
 MAX_DEGREE: int = LUT_TERMS
 # Per-head Lion forget factors of the full path, heads 0..7 (sdpc_kernel.py:1416).
 MULTI_SCALE_LAMBDA = list(V10_LION_LAMBDA)
+# Most Chebyshev coefficients the fixed-coefficient (fast) path evaluates.
+MAX_FAST_TERMS = 16
 
 _lut_lock = threading.Lock()
 _lut_by_device: dict = {}
@@ -157,10 +159,13 @@ def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_m
             beta2=lion_beta2, weight_decay=lion_wd, chunk_size=chunk_size, gate_global=gate_global,
             dynamic_lambda=dynamic_lambda, use_lut=use_lut)
         return out, c_new, m_new
-    if coeffs.shape[2] > 8:
-        # The reference's PyTorch fast path evaluates any number of terms; its
-        # kernels (and its engine, max_degree <= 8) stop at eight.
-        raise ValueError(f"the fast path supports at most 8 Chebyshev coefficients, got {coeffs.shape[2]}")
+    if coeffs.shape[2] > MAX_FAST_TERMS:
+        # The reference's PyTorch fast path evaluates any number of terms
+        # (sdpc_kernel.py:1751-1776); its Triton kernels and its engine
+        # (max_degree <= 8) stop at eight.  Here the fixed-coefficient kernels
+        # take up to 16 (more than 8 by Clenshaw).
+        raise ValueError(f"the fast path supports at most {MAX_FAST_TERMS} Chebyshev coefficients, "
+                         f"got {coeffs.shape[2]}")
     damping = v10_damping(H, x.device)
     lam = head_momentum(ema_momentum, H, x.device)
     if torch.is_grad_enabled() and (x.requires_grad or coeffs.requires_grad):

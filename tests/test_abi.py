@@ -77,23 +77,42 @@ def test_workspace_bytes_formula():
     # dynamic lambda: 256-token tiles, two words (A and B) per lane
     a.g = 0x10000
     assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 64 * 64 * 16
+    # more than 8 coefficients, or rows off 4-element boundaries, or a head
+    # size that is not a multiple of 4: the one-lane geometry, 128-token tiles
     a.K = 9
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 128 * 64 * 16
+    a.K, a.g = 8, None
+    a.x_stride_s = 514
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 128 * 64 * 8
+    a.x_stride_s, a.hd = 512, 62              # D = 496: 8 lane-blocks per row, the last one partial
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 128 * 64 * 8
+    a.hd, a.K = 64, 17
     assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 0
+
+
+def test_coefficient_limits_per_entry_point():
+    lib = nat.load()
+    for K in (9, 16):
+        assert lib.osm_workspace_bytes(ctypes.byref(_args(K=K)), nat.OP_FWD) > 0
+        assert lib.osm_workspace_bytes(ctypes.byref(_args(K=K)), nat.OP_BWD) > 0
+        assert lib.osm_workspace_bytes(ctypes.byref(_args(K=K)), nat.OP_TTT) == 0     # the TTT takes K <= 8
+        assert b"TTT" in lib.osm_last_error()
+    assert nat.MAX_K == 16 and nat.MAX_K_TTT == 8
 
 
 @pytest.mark.parametrize("kw,code", [
     (dict(abi_version=99), -1),
     (dict(flags=0x100), -1),
     (dict(K=0), -2),
-    (dict(K=9), -2),
-    (dict(hd=6), -2),
+    (dict(K=17), -2),
+    (dict(hd=0), -2),
     (dict(H=0), -2),
     (dict(S=-1), -2),
     (dict(x_dtype=7), -3),
     (dict(out_dtype=2), -3),
     (dict(x=0), -1),
-    (dict(x=0x10004), -4),          # not 16-byte aligned for fp32
-    (dict(x_stride_s=510), -4),
+    (dict(x=0x10002), -4),          # not aligned to one fp32 element
+    (dict(x_stride_s=-512), -4),
     (dict(out_stride_b=-4), -4),
 ])
 def test_argument_errors(kw, code):
@@ -127,6 +146,10 @@ def test_bwd_workspace_bytes_formula():
     # lane, then K-padded partials per tile.
     slots = (2048 + 32 * 86 * 64 * 16 + 255) // 256 * 256
     assert lib.osm_workspace_bytes(ctypes.byref(a), nat.OP_BWD) == slots + 32 * 86 * 8 * 64 * 4
+    # more than 8 coefficients: 96-token tiles (171 at S=16384), 16 padded
+    a.K = 12
+    slots = (2048 + 32 * 171 * 64 * 16 + 255) // 256 * 256
+    assert lib.osm_workspace_bytes(ctypes.byref(a), nat.OP_BWD) == slots + 32 * 171 * 16 * 64 * 4
     assert lib.osm_workspace_bytes(ctypes.byref(a), 3) == 0
     assert b"osm_op" in lib.osm_last_error()
 
@@ -144,13 +167,13 @@ def _bwd(**kw):
 @pytest.mark.parametrize("akw,bkw,code", [
     ({}, dict(grad_out=0), -1),
     ({}, dict(grad_x=0), -1),
-    ({}, dict(grad_x=0x10004), -4),
-    ({}, dict(go_stride_s=510), -4),
+    ({}, dict(grad_x=0x10002), -4),          # not aligned to one element
+    ({}, dict(go_stride_s=-512), -4),
     ({}, dict(gx_stride_s=256), -4),          # rows overlap
     ({}, dict(gx_stride_b=512), -4),          # batches overlap
     (dict(out=0), {}, -1),                    # the clamp mask needs the saved output
     (dict(out=0, flags=nat.FLAG_NO_CLAMP), {}, -5),   # ... unless there is no clamp: reaches the workspace check
-    (dict(K=9), {}, -2),
+    (dict(K=17), {}, -2),
 ])
 def test_bwd_argument_errors(akw, bkw, code):
     lib = nat.load()
@@ -197,13 +220,13 @@ def test_v10_argument_errors(kw, code):
 def test_error_messages_are_thread_local():
     import threading
     lib = nat.load()
-    a = _args(K=9)
+    a = _args(K=17)
     assert lib.osm_cheby_ema_fwd(ctypes.byref(a), None, 0, None) == -2
     seen = []
     t = threading.Thread(target=lambda: seen.append(lib.osm_last_error()))
     t.start()
     t.join()
-    assert seen == [b""] and b"K=9" in lib.osm_last_error()
+    assert seen == [b""] and b"K=17" in lib.osm_last_error()
 
 
 def _doc_struct(name):

@@ -41,9 +41,10 @@ def test_cpu_tensor_raises():
         apply_cheby_rkv_v10(x, c, None, n_heads=4)
 
 
-def test_fast_path_rejects_more_than_eight_coefficients():
-    # the reference's kernels clamp the degree to 8 (sdpc_kernel.py:2379)
+def test_fast_path_rejects_more_than_sixteen_coefficients():
+    # the reference's PyTorch fast path takes any number of terms; the
+    # fixed-coefficient kernels here take up to 16
     x = torch.randn(1, 16, 32)
-    c = torch.randn(1, 4, 10, 8)
-    with pytest.raises(ValueError, match="at most 8"):
+    c = torch.randn(1, 4, 17, 8)
+    with pytest.raises(ValueError, match="at most 16"):
         apply_cheby_rkv_v10(x, c, torch.zeros_like(c), n_heads=4, seq_threshold=384)
