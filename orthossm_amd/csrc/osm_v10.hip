@@ -28,6 +28,17 @@ namespace {
 
 constexpr int kBlockTok = kV10Groups * kV10Run;      // 256 tokens per block
 constexpr float kLog2e = 1.4426950408889634f;
+// Floats per LUT row in LDS: the 8 values of T_k padded to 12, so that the
+// 16-byte reads of random rows by the lanes of a wave spread over more LDS
+// banks than with 8 (rows i and i' collide when 12 (i - i') = 0 mod the
+// bank count).  Measured at the configs[1] shape on MI355X: 221 against
+// 227 us with the XCD order below.
+constexpr int kLutStride = 12;
+// Workgroup order: the workgroups whose lanes share 128-byte lines of x go
+// to one XCD, so each line is fetched into one L2 (with consecutive indices
+// the 4 workgroups of a line sat on 4 XCDs and every line was fetched 4
+// times): 227 against 270 us at the configs[1] shape.
+constexpr bool kXcdLines = true;
 
 // x rounded to bf16 (round to nearest even), as the reference casts on entry.
 template <typename XT>
@@ -52,7 +63,7 @@ __device__ __forceinline__ void v10_softsign(float xb, float& absu, float& sgn) 
 template <int LW>
 struct V10Lds {
   static constexpr int NW = kV10Groups * LW / 64;   // waves per workgroup
-  float lut[256][8];                 // T_k at the table's grid, k contiguous
+  float lut[256][kLutStride];        // T_k at the table's grid, k contiguous
   float cs[8][LW];                   // coefficients of the current chunk
   float ms[8][LW];                   // Lion momentum
   float wA[NW][LW], wB[NW][LW];      // each wave's composed EMA map over its runs
@@ -73,8 +84,24 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
   const int tid = threadIdx.x;
   const int l = tid % LW, g = tid / LW;
   const int wave = tid >> 6, gw = (tid & 63) / LW;   // run inside the wave
-  const int lg = blockIdx.x % p.n_lg;
-  const int bh = blockIdx.x / p.n_lg;
+  int lg = blockIdx.x % p.n_lg;
+  int bh = blockIdx.x / p.n_lg;
+  if constexpr (kXcdLines) {
+    // Workgroups go to the 8 XCDs round-robin by index.  The 128 / (4 LW)
+    // consecutive lane groups of a head that share 128-byte lines of x (fp32)
+    // are given indices with the same residue mod 8, so their lines are
+    // fetched into one XCD's L2 once.
+    constexpr int kShare = 128 / (4 * LW);
+    const int grid = gridDim.x;
+    if (p.n_lg % kShare == 0 && grid % (8 * kShare) == 0) {
+      const int v = blockIdx.x, xcd = v & 7, slot = v >> 3;
+      const int line = (slot / kShare) * 8 + xcd;          // line group, global
+      const int q = slot % kShare;
+      const int lines_per_head = p.n_lg / kShare;
+      lg = (line % lines_per_head) * kShare + q;
+      bh = line / lines_per_head;
+    }
+  }
   const int h = bh % p.H, b = bh / p.H;
   const int j = lg * LW + l;                 // lane inside the head
   const bool lane_ok = j < p.hd;
