@@ -162,10 +162,20 @@ def measured_traffic(workload: str):
         return None
 
 
-# Kernels whose HBM traffic the summary reports (the dominant kernel of each
-# workload), and the auxiliary kernels of a step (tile merges / reductions).
-MAIN_KERNELS = ("cheby_ema_fwd_kernel", "cheby_ema_ttt_kernel", "cheby_ema_bwd_kernel", "v10_chunked_kernel")
+# The auxiliary kernels of a step (tile merges / reductions).
 AUX_KERNELS = ("ttt_merge", "ttt_finalize", "bwd_reduce")
+
+
+def main_kernel(cfg) -> str:
+    """Name fragment of the workload's dominant kernel (the backward
+    workload also runs forward launches to produce its saved outputs)."""
+    if cfg.v10:
+        return "v10_chunked_kernel"
+    if cfg.bwd:
+        return "cheby_ema_bwd_kernel"
+    if cfg.ttt:
+        return "cheby_ema_ttt_kernel"
+    return "cheby_ema_fwd_kernel"
 READ_COUNTERS = ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_BUBBLE_sum")
 WRITE_COUNTERS = ("TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum")
 
@@ -226,7 +236,7 @@ def pmc_summary(read_path: str, write_path: str, workload: str) -> dict:
     for key, path, fn, names in (("read", read_path, read_bytes, READ_COUNTERS),
                                  ("write", write_path, write_bytes, WRITE_COUNTERS)):
         disp = list(_dispatch_counters(path).values())
-        main = [fn(c) for k, c in disp if any(m in k for m in MAIN_KERNELS)]
+        main = [fn(c) for k, c in disp if main_kernel(cfg) in k]
         aux = [fn(c) for k, c in disp if any(m in k for m in AUX_KERNELS)]
         copies = [fn(c) for k, c in disp if "copyBuffer" in k][-5:]
         if not main or len(copies) < 5:
@@ -237,8 +247,8 @@ def pmc_summary(read_path: str, write_path: str, workload: str) -> dict:
         # auxiliary kernels of a step, per launch of the main kernel
         out[f"{key}_aux_bytes"] = sum(aux) / len(main) if aux else 0.0
         out[f"copy_{key}_ratio"] = (sum(copies) / len(copies)) / copy_bytes
-        out[f"{key}_counters_mean"] = {n: sum(c.get(n, 0.0) for k, c in disp if any(m in k for m in MAIN_KERNELS))
-                                       / len(main) for n in names}
+        out[f"{key}_counters_mean"] = {n: sum(c.get(n, 0.0) for k, c in disp if main_kernel(cfg) in k) / len(main)
+                                       for n in names}
     out["bytes"] = out["read_bytes"] + out["write_bytes"]
     out["step_bytes"] = out["bytes"] + out["read_aux_bytes"] + out["write_aux_bytes"]
     out["algorithmic_bytes"] = algorithmic_bytes(cfg) / launches
