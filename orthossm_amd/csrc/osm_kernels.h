@@ -74,20 +74,21 @@ struct FwdShape {
 // on 4-element boundaries, or more than 8 coefficients).
 FwdShape fwd_geometry(bool dyn, int64_t B, int64_t D, int64_t S, bool generic);
 
-// TTT: keeps the raw x and r = 1/(1+exp(2 damping p)) of every token of the
-// run in registers, plus 2K gradient accumulators per lane: one lane per
-// thread (half the accumulators of two).  Measured on MI355X at BASELINE
-// configs[4] (bf16): 20-token runs 1085 us against 1131 with 16 (the
-// per-thread setup, chain, composition and reduction amortised over more
-// tokens), although at the 128-VGPR bound of two workgroups per CU the
-// compiler spills 5 registers; 18 tokens 1104 us, 22 tokens (13 spilled)
-// 1141, 24 tokens (21 spilled) 1355; 2 lanes x 8 or 16 tokens +10-20%.
+// TTT: keeps the raw x and w = (1-lam)(1-2r) (r = 1/(1+exp(2 damping p)))
+// of every token of the run in registers, u = softsign(x) in LDS, plus 2K
+// gradient accumulators per lane: one lane per thread (half the
+// accumulators of two).  Measured on MI355X at BASELINE configs[4] (bf16),
+// with u in LDS: 24-token runs 1001-1008 us against 1047-1056 with 20, 1025
+// with 28 and 1092-1095 with 16 (longer runs amortise the per-thread setup,
+// chain, composition and reduction over more tokens; at the 128-VGPR bound
+// of two workgroups per CU the compiler spills 19 registers at 24 tokens,
+// mostly on the rare slow path, and 40 at 28); 2 lanes x 8 or 16 tokens
+// +10-20% (an earlier version).
 // One look-back word per thread (checkpoints every 8 tiles): the kernel is
 // VALU-bound, and every thread runs the polling code of each of its words
 // (at 16-token runs 1147 us with two words against 1254 with eight and 1177
-// with four; at 20-token runs one word 1069 against 1086 with two, which
-// also spills one register more).
-using TttTile = TileGeo<1, 8, 20, 64, 1>;   // 160 tokens
+// with four; at 20-token runs one word 1069 against 1086 with two).
+using TttTile = TileGeo<1, 8, 24, 64, 1>;   // 192 tokens
 int ttt_tile_tokens(bool dyn, int x_dtype);
 
 // Backward: one lane per thread (the clamp mask makes the adjoint map's A

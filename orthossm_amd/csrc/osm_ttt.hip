@@ -33,12 +33,13 @@ __host__ __device__ constexpr int n_fields() {
   return 2 * KP + 2;  // P_0..P_{KP-1}, Q_0..Q_{KP-1}, Ar (beta), Br (alpha)
 }
 
-// Raw x of a thread's run (R tokens x LPT lanes), kept between the passes.
+// Raw x of a thread's run (R tokens x LPT lanes), kept between the passes
+// (pass 2 needs x as the target y and for the NaN checks of its slow path).
 // Pass 1 reads row r with first(r, i), then calls seal(r): from then on the
 // row is read with get(r, i).  seal() hides the value from the compiler, so
-// pass 2 re-derives u from it instead of keeping pass 1's unpacked x and u
-// alive across the look-back (twice the registers); for bf16 with one lane
-// per thread it also packs two tokens per register.
+// it keeps the raw x instead of pass 1's unpacked values alive across the
+// look-back; for bf16 with one lane per thread it also packs two tokens per
+// register.
 template <typename XT, int R, int LPT>
 struct XRun;
 
@@ -127,9 +128,10 @@ struct RunGrad {
 // ema_final capture; the fast variant assumes none of them occurs in the run.
 template <class G, bool DYN, bool SOFT, bool SLOW, typename XT, typename OT, int KP>
 __device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G::LPT], const XRun<XT, G::R, G::LPT>& xr,
-                                          const float (&rr)[G::R][G::LPT], const float (&lamv)[G::R],
-                                          const float (&y_after)[G::LPT], const TileAddr& a, float lo, float hi,
-                                          int t_first, int S, bool clamp, bool nan_zero_u, float* fin) {
+                                          const float* ul, const float (&rr)[G::R][G::LPT],
+                                          const float (&lamv)[G::R], float om2, const float (&y_after)[G::LPT],
+                                          const TileAddr& a, float lo, float hi, int t_first, int S, bool clamp,
+                                          bool nan_zero_u, float* fin) {
   constexpr int R = G::R, LPT = G::LPT;
 #pragma unroll
   for (int k = 0; k < KP; ++k)
@@ -138,25 +140,31 @@ __device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G:
 #pragma unroll
   for (int i = 0; i < LPT; ++i) rg.al[i] = 0.0f;
   rg.Lp = 1.0f;
-  float u[LPT];
-#pragma unroll
-  for (int i = 0; i < LPT; ++i) u[i] = softsign_fast(xr.get(0, i));
+  f32x4 ug[LPT];   // u of tokens 4m .. 4m+3 of each lane
+  // Under a static lambda the products Lp are lambda^r, which the compiler
+  // would otherwise share with pass 1's run aggregate and keep in registers
+  // across the look-back; a hidden copy of lambda keeps them here.
+  float lam_lp = lamv[0];
+  if constexpr (!DYN) asm volatile("" : "+v"(lam_lp));
   uint32_t so = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const float lam = lamv[r];
     const float one_m = 1.0f - lam;
     const float n2 = -2.0f * one_m;
-    if (r > 0) rg.Lp *= lam;
-    float un[LPT], yn[LPT];
+    if (r > 0) rg.Lp *= DYN ? lam : lam_lp;
+    if (r % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < LPT; ++i) ug[i] = *reinterpret_cast<const f32x4*>(ul + i * R + r);
+    }
+    float yn[LPT];
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       if (r + 1 < R) {
-        const float xn = xr.get(r + 1, i);
-        un[i] = softsign_fast(xn);
-        yn[i] = SOFT ? ((xn == xn) ? un[i] : xn) : xn;
+        // softsign target: u of the next token (NaN where x is NaN, as x)
+        if constexpr (SOFT) yn[i] = r % 4 != 3 ? ug[i][(r + 1) % 4] : ul[i * R + r + 1];
+        else yn[i] = xr.get(r + 1, i);
       } else {
-        un[i] = 0.0f;
         yn[i] = y_after[i];
       }
     }
@@ -164,12 +172,20 @@ __device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G:
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const float rv = rr[r][i];
-      s[i] = __builtin_fmaf(lam, s[i], __builtin_fmaf(n2, rv, one_m));
-      o[i] = __builtin_amdgcn_fmed3f(s[i], lo, hi);
+      float D;
+      if constexpr (DYN) {
+        s[i] = __builtin_fmaf(lam, s[i], __builtin_fmaf(n2, rv, one_m));
+        D = __builtin_fmaf(-rv, rv, rv) * one_m;   // (1 - lam) r (1 - r) = (1 - lam)(1 - z^2) / 4
+      } else {
+        // rv is w = (1 - lam) z: s = lam s + w, D = (1 - lam)^2 - w^2 = (1 - lam)^2 (1 - z^2)
+        s[i] = __builtin_fmaf(lam, s[i], rv);
+        D = __builtin_fmaf(-rv, rv, om2);
+      }
+      // On the fast path |s| <= 1 over the run (or the clamp is off), so the
+      // clamp is the identity there.
+      o[i] = SLOW ? __builtin_amdgcn_fmed3f(s[i], lo, hi) : s[i];
       float e = o[i] - yn[i];
-      float D = __builtin_fmaf(-rv, rv, rv);   // r (1 - r) = (1 - z^2) / 4
-      if constexpr (DYN) D *= one_m;
-      float uu = u[i];
+      float uu = ug[i][r % 4];
       if constexpr (SLOW) {
         const int t = t_first + r;
         const bool pass = !clamp || __builtin_fabsf(s[i]) <= 1.0f;
@@ -197,11 +213,33 @@ __device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G:
         vm2 = vm1;
         vm1 = vk;
       }
-      u[i] = un[i];
     }
     BufVec<OT, LPT>::store(a.out, a.vo, so, o);
     so = next_off(so, a.so);
+
   }
+}
+
+// x^N by repeated squaring.
+template <int N>
+__device__ __forceinline__ float pow_n(float x) {
+  if constexpr (N == 0) return 1.0f;
+  else if constexpr (N == 1) return x;
+  else {
+    const float h = pow_n<N / 2>(x);
+    return N % 2 ? h * h * x : h * h;
+  }
+}
+
+// Per-lane scale of the gradient sums: 2/N and the constant part of the
+// derivative (1-lam) damping (1-z^2): 4 damping times D = (1-lam) r (1-r)
+// (dynamic lambda), damping / (1-lam) times D = (1-lam)^2 (1-z^2) (static; 0
+// at lam = 1, where D is 0).
+template <bool DYN>
+__device__ __forceinline__ float ttt_lane_scale(const FwdParams& p, int h) {
+  if constexpr (DYN) return p.ttt_scale * 4.0f * p.damping[h];
+  const float lam = p.lam[h];
+  return lam != 1.0f ? p.ttt_scale * p.damping[h] / (1.0f - lam) : 0.0f;
 }
 
 // Sum over the token groups of a wave (lanes wl, wl ^ TPR, ...).
@@ -221,13 +259,19 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   constexpr int NTG = G::NTG;
   constexpr int F = n_fields<KP>();
   static_assert(G::LANES == kLanes, "partials and merges assume 64-lane lane-blocks");
+  static_assert(R % 4 == 0, "u moves through LDS four tokens at a time");
   __shared__ ChainLds<G> L;
   __shared__ float mono[KP][kLanes];
   __shared__ float sh_y0[NTG][kLanes];      // target y at each run's first token
   __shared__ float sh_lam0[NTG][G::TPR];    // lambda at each run's first token
   __shared__ float sh_al[NTG][kLanes];      // run adjoint maps a[t0] = alpha + beta rho
   __shared__ float sh_be[NTG][G::TPR];
-  __shared__ float sh_red[G::WAVES][2 * KP][kLanes];
+  // u of every element of the tile (pass 1 -> pass 2 of the same wave), then
+  // the per-wave gradient sums (after the barrier that follows pass 2).
+  __shared__ union {
+    float u[NTG][G::LANES][R];   // [token group][lane][token of the run]
+    float red[G::WAVES][2 * KP][kLanes];
+  } sh_ur;
 
   const ThreadPos q = thread_pos<G>();
   const Tags tags = launch_tags(p.hdr);
@@ -274,7 +318,10 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   float c[LPT][KP];
   mono_read<G, KP>(mono, q, c);
 
-  // Pass 1: r = 1/(1+exp(2 damping p)) per element and the run aggregate.
+  // Pass 1: r = 1/(1+exp(2 damping p)) per element (kept as w = (1-lam)(1-2r)
+  // = (1-lam) z under a static lambda) and the run aggregate; u to LDS.
+  float* const ul = &sh_ur.u[q.tg][q.lt * LPT][0];
+  f32x4 uw[LPT];
   float rr[R][LPT];
   float A = 1.0f;
   float Bv[LPT];
@@ -289,12 +336,18 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     const float n2 = -2.0f * one_m;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      rr[r][i] = tanh_r(horner<KP>(softsign_fast(xr.first(r, i)), c[i]));
-      Bv[i] = __builtin_fmaf(lam, Bv[i], __builtin_fmaf(n2, rr[r][i], one_m));
+      const float u = softsign_fast(xr.first(r, i));
+      uw[i][r % 4] = u;
+      if (r % 4 == 3) *reinterpret_cast<f32x4*>(ul + i * R + r - 3) = uw[i];
+      const float rv = tanh_r(horner<KP>(u, c[i]));
+      const float w = __builtin_fmaf(n2, rv, one_m);
+      rr[r][i] = DYN ? rv : w;
+      Bv[i] = __builtin_fmaf(lam, Bv[i], w);
     }
-    A *= lam;
+    if constexpr (DYN) A *= lam;
     xr.seal(r);
   }
+  if constexpr (!DYN) A = pow_n<R>(lam_h);
   bool bad = false;
 #pragma unroll
   for (int i = 0; i < LPT; ++i) bad |= Bv[i] != Bv[i];
@@ -309,8 +362,12 @@ cheby_ema_ttt_kernel(const FwdParams p) {
 #pragma unroll
       for (int i = 0; i < LPT; ++i) {
         const float x = xr.get(r, i);
-        if (x != x) rr[r][i] = p.nan_zero_u ? tanh_r(c[i][0]) : 0.5f;
-        Bv[i] = __builtin_fmaf(lamv[r], Bv[i], __builtin_fmaf(-2.0f * one_m, rr[r][i], one_m));
+        if (x != x) {
+          const float rv = p.nan_zero_u ? tanh_r(c[i][0]) : 0.5f;
+          rr[r][i] = DYN ? rv : __builtin_fmaf(-2.0f * one_m, rv, one_m);
+        }
+        const float w = DYN ? __builtin_fmaf(-2.0f * one_m, rr[r][i], one_m) : rr[r][i];
+        Bv[i] = __builtin_fmaf(lamv[r], Bv[i], w);
       }
     }
   }
@@ -347,30 +404,33 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   }
 
   // Pass 2 from the carried state.
+  // |s| <= 1 at the run start keeps |s| <= 1 over the run when 0 <= lambda
+  // <= 1 (s is then a convex combination of it and values of tanh, and the
+  // fp32 update cannot round past 1), so the clamp can only bind if the
+  // carried state is already out of range; with the clamp off it is the
+  // identity except on NaN.  The fast path assumes neither happens.
+  const bool clamp = p.clamp_out != 0;
   float s[LPT];
-  bool big = false;
+  bool big = DYN ? !(p.lam_min >= 0.0f && p.lam_max <= 1.0f) : !(lam_h >= 0.0f && lam_h <= 1.0f);
 #pragma unroll
   for (int i = 0; i < LPT; ++i) {
     s[i] = __builtin_fmaf(pA, L.carry[q.lt * LPT + i], pB[i]);
-    big |= __builtin_fabsf(s[i]) > 1.0f;
+    big |= clamp ? !(__builtin_fabsf(s[i]) <= 1.0f) : s[i] != s[i];
   }
-  // |s| <= 1 at the run start keeps |s| <= 1 over the run (s is a convex
-  // combination of it and values of tanh), so the clamp can only bind if the
-  // carried state is already out of range.
-  const bool clamp = p.clamp_out != 0;
   const float lo = clamp ? -1.0f : -__builtin_inff();
   const float hi = clamp ? 1.0f : __builtin_inff();
   const int t_first = ti.tile * G::TILE + q.tg * R;
   float* fin = (ti.is_last && p.ema_final && a.vo != kOffOOB)
                    ? p.ema_final + (int64_t)ti.b * p.D + ti.lbd * kLanes + q.lt * LPT
                    : nullptr;
+  const float om2 = (1.0f - lam_h) * (1.0f - lam_h);
   RunGrad<KP, LPT> rg;
-  if (bad || (clamp && big) || ti.is_last)
-    ttt_pass2<G, DYN, SOFT, true, XT, OT, KP>(rg, s, xr, rr, lamv, y_after, a, lo, hi, t_first, p.S, clamp,
-                                               p.nan_zero_u != 0, fin);
+  if (bad || big || ti.is_last)
+    ttt_pass2<G, DYN, SOFT, true, XT, OT, KP>(rg, s, xr, ul, rr, lamv, om2, y_after, a, lo, hi, t_first, p.S,
+                                               clamp, p.nan_zero_u != 0, fin);
   else
-    ttt_pass2<G, DYN, SOFT, false, XT, OT, KP>(rg, s, xr, rr, lamv, y_after, a, lo, hi, t_first, p.S, clamp,
-                                                false, fin);
+    ttt_pass2<G, DYN, SOFT, false, XT, OT, KP>(rg, s, xr, ul, rr, lamv, om2, y_after, a, lo, hi, t_first,
+                                                p.S, clamp, false, fin);
 
   // Compose the runs of the tile: rho of run g = Ar_g + Br_g rho_tile.
   const float beta = rg.Lp * lam_after;
@@ -387,8 +447,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     for (int i = 0; i < LPT; ++i) Ar[i] = __builtin_fmaf(bg, Ar[i], sh_al[g][q.lt * LPT + i]);
     Br *= bg;
   }
-  // Per-lane scale: 2/N and the constant part of D = 4 damping (1-lam) r(1-r).
-  const float ks = p.ttt_scale * 4.0f * p.damping[a.h] * (DYN ? 1.0f : 1.0f - lam_h);
+  const float ks = ttt_lane_scale<DYN>(p, a.h);
   float* part = p.partials + ((size_t)ti.lb * p.n_tiles + ti.tile) * F * kLanes;
   if (q.tg == 0) {
     // Tile map: a[tile start] = al_0 + beta_0 (Ar_0 + Br_0 rho_tile).
@@ -398,26 +457,30 @@ cheby_ema_ttt_kernel(const FwdParams p) {
       part[(size_t)(2 * KP + 1) * kLanes + q.lt * LPT + i] = __builtin_fmaf(beta, Ar[i], rg.al[i]);
     }
   }
-  // Run contributions P + lam_after F (Ar + Br rho_tile), summed over runs.
-  const float cB = lam_after * Br * ks;
+  // Run contributions P + lam_after F (Ar + Br rho_tile), summed over runs;
+  // the per-lane scale is applied to the sums.
+  const float cB = lam_after * Br;
 #pragma unroll
   for (int k = 0; k < KP; ++k) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const float pv = wave_sum_tg<G>(ks * __builtin_fmaf(lam_after * Ar[i], rg.F[k][i], rg.P[k][i]));
+      const float pv = wave_sum_tg<G>(__builtin_fmaf(lam_after * Ar[i], rg.F[k][i], rg.P[k][i]));
       const float qv = wave_sum_tg<G>(cB * rg.F[k][i]);
       if (q.wl < G::TPR) {
-        sh_red[q.wave][k][q.lt * LPT + i] = pv;
-        sh_red[q.wave][KP + k][q.lt * LPT + i] = qv;
+        sh_ur.red[q.wave][k][q.lt * LPT + i] = pv;
+        sh_ur.red[q.wave][KP + k][q.lt * LPT + i] = qv;
       }
     }
   }
   __syncthreads();
+  // scale of lane wl (the thread's own lane when LPT = 1)
+  const int dw = ti.lbd * kLanes + q.wl;
+  const float ks_w = LPT == 1 ? ks : ttt_lane_scale<DYN>(p, dw < p.D ? div_hd(dw, p) : 0);
   for (int v = q.wave; v < 2 * KP; v += G::WAVES) {
     float acc = 0.0f;
 #pragma unroll
-    for (int w = 0; w < G::WAVES; ++w) acc += sh_red[w][v][q.wl];
-    part[(size_t)v * kLanes + q.wl] = acc;
+    for (int w = 0; w < G::WAVES; ++w) acc += sh_ur.red[w][v][q.wl];
+    part[(size_t)v * kLanes + q.wl] = ks_w * acc;
   }
   finish_block(p.hdr, tags.epoch);
 }
