@@ -238,8 +238,9 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
     for (int r = R - 1; r >= 0; --r) {
       const float lam = DYN ? lamv[r] : lam_h;
       Bv[0] = lam * (gv[r] + Bv[0]);
-      A *= lam;
+      if constexpr (DYN) A *= lam;
     }
+    if constexpr (!DYN) A = pow_n<R>(lam_h);
   } else {
     // Tokens >= S (last tile) are the identity; a zero mask cuts the chain.
 #pragma unroll

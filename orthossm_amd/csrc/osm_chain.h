@@ -124,17 +124,12 @@ __device__ __forceinline__ LaneSlots lane_slots(unsigned long long* slots, const
   return s;
 }
 
-// Aggregate A of a full tile under a static lambda, in the same
-// multiplication order as the producing workgroup's scan.
+// Aggregate A of a full tile under a static lambda, lambda^TILE rounded once
+// (the producing workgroup publishes only B and uses the same value for its
+// checkpoint; an error in A would repeat at every tile of the carry chain).
 template <class G>
 __device__ __forceinline__ float static_tile_A(float lam) {
-  float a = 1.0f;
-#pragma unroll
-  for (int r = 0; r < G::R; ++r) a *= lam;
-  float A = 1.0f;
-#pragma unroll
-  for (int q = 0; q < G::NTG; ++q) A *= a;
-  return A;
+  return pow_n<G::TILE>(lam);
 }
 
 // Token-group scan.  In: this thread's run aggregate (A, Bv).  Out: (pA, pB)
@@ -209,18 +204,19 @@ __device__ __forceinline__ void look_back_issue(LookBack<G, DYN>& st, const Thre
   if (q.wave < G::NSUB && st.g0 > 0) st.vck = peek(ls.at(st.g0 - 1, carry_lane<G>(q)));
 }
 
-// `lam_look` is the static lambda of look_lane (unused when DYN); `init_carry`
+// `a_look` is the full-tile decay static_tile_A of look_lane's static lambda
+// (unused when DYN); `init_carry`
 // the initial state of carry_lane (waves < NSUB).
 template <class G, bool DYN>
 __device__ __forceinline__ void look_back_finish(LookBack<G, DYN>& st, ChainLds<G>& L, const ThreadPos& q,
                                                  const TileInfo& ti, const Tags& tg, float aggA, float aggB,
-                                                 const LaneSlots& ls, float init_carry, float lam_look,
+                                                 const LaneSlots& ls, float init_carry, float a_look,
                                                  unsigned* hdr_words) {
   if (ti.tile > 0) {
     const int ll = look_lane<G>(q);
     float mA = 1.0f, mB = 0.0f;
     if (st.beg < st.end) {
-      const float Afull = DYN ? 1.0f : static_tile_A<G>(lam_look);
+      const float Afull = DYN ? 1.0f : a_look;
 #pragma unroll
       for (int i = 0; i < G::WPT; ++i) {
         if (st.beg + i < st.end) {

@@ -376,6 +376,27 @@ __device__ __forceinline__ float clenshaw_u(float u, const float (&d)[N]) {
   return b1;
 }
 
+// x^N by repeated squaring in float64, rounded once to fp32 (within about
+// half an ulp of the exact power; a float chain of N products, or squaring in
+// fp32, errs by several ulps, and over a long sequence the carried state
+// accumulates that error tile after tile when lambda is close to 1).  Under a
+// static lambda the kernels form the decay of an R-token run as
+// pow_n<R>(lambda) and that of a full tile, for checkpoints and the
+// look-back alike, as pow_n<TILE>(lambda) (static_tile_A).
+template <int N>
+__device__ __forceinline__ double pow_n_f64(double x) {
+  if constexpr (N == 0) return 1.0;
+  else if constexpr (N == 1) return x;
+  else {
+    const double h = pow_n_f64<N / 2>(x);
+    return N % 2 ? h * h * x : h * h;
+  }
+}
+template <int N>
+__device__ __forceinline__ float pow_n(float x) {
+  return (float)pow_n_f64<N>((double)x);
+}
+
 // Given y2 = 2*log2(e) * damping * p, returns r = 1 / (1 + exp(2*damping*p));
 // then tanh(damping*p) = 1 - 2r.  exp2 overflow to +Inf gives r = 0 (z = 1);
 // underflow to 0 gives r = 1 (z = -1).

@@ -192,9 +192,10 @@ cheby_ema_fwd_kernel(const FwdParams p) {
         w[r0 + rr][i] = __builtin_fmaf(n2, tanh_r(py[rr][i]), one_m);
         Bv[i] = __builtin_fmaf(lam, Bv[i], w[r0 + rr][i]);
       }
-      A *= lam;
+      if constexpr (DYN) A *= lam;
     }
   }
+  if constexpr (!DYN) A = pow_n<R>(lam_h);
   bool bad = false;
 #pragma unroll
   for (int i = 0; i < LPT; ++i) bad |= Bv[i] != Bv[i];
@@ -207,11 +208,14 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   {
     const int dc = ti.lbd * G::LANES + carry_lane<G>(q);
     const float init_c = (p.ema_init && q.wave < G::NSUB && dc < p.D) ? p.ema_init[(int64_t)ti.b * p.D + dc] : 0.0f;
+    // static lambda: the tile's decay as the look-back recomputes it
+    if constexpr (!DYN)
+      if (q.wave < G::NSUB) aggA = static_tile_A<G>(p.lam[dc < p.D ? div_hd(dc, p) : 0]);
     const int dlk = ti.lbd * G::LANES + look_lane<G>(q);
-    const float lam_look = DYN ? 0.0f : p.lam[dlk < p.D ? div_hd(dlk, p) : 0];
+    const float a_look = DYN ? 0.0f : static_tile_A<G>(p.lam[dlk < p.D ? div_hd(dlk, p) : 0]);
     LookBack<G, DYN> lbk;
     look_back_issue<G, DYN>(lbk, q, ti, ls);
-    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, lam_look, p.hdr);
+    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, a_look, p.hdr);
   }
   finish_complete(p.hdr, tags.epoch, fin_prev);
 

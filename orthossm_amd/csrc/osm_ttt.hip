@@ -220,17 +220,6 @@ __device__ __forceinline__ void ttt_pass2(RunGrad<KP, G::LPT>& rg, float (&s)[G:
   }
 }
 
-// x^N by repeated squaring.
-template <int N>
-__device__ __forceinline__ float pow_n(float x) {
-  if constexpr (N == 0) return 1.0f;
-  else if constexpr (N == 1) return x;
-  else {
-    const float h = pow_n<N / 2>(x);
-    return N % 2 ? h * h * x : h * h;
-  }
-}
-
 // Per-lane scale of the gradient sums: 2/N and the constant part of the
 // derivative (1-lam) damping (1-z^2): 4 damping times D = (1-lam) r (1-r)
 // (dynamic lambda), damping / (1-lam) times D = (1-lam)^2 (1-z^2) (static; 0
@@ -266,6 +255,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   __shared__ float sh_lam0[NTG][G::TPR];    // lambda at each run's first token
   __shared__ float sh_al[NTG][kLanes];      // run adjoint maps a[t0] = alpha + beta rho
   __shared__ float sh_be[NTG][G::TPR];
+  __shared__ float sh_pw[2][kLanes];        // static lambda: run and tile decay of each lane
   // u of every element of the tile (pass 1 -> pass 2 of the same wave), then
   // the per-wave gradient sums (after the barrier that follows pass 2).
   __shared__ union {
@@ -314,6 +304,14 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   }
 
   mono_store<KP, G>(ml, q, mono);
+  if constexpr (!DYN) {
+    // lambda^R and lambda^TILE of each lane, by the last two waves
+    if (q.wave >= G::WAVES - 2) {
+      const int d = ti.lbd * kLanes + q.wl;
+      const float lam = p.lam[d < p.D ? div_hd(d, p) : 0];
+      sh_pw[q.wave - (G::WAVES - 2)][q.wl] = q.wave == G::WAVES - 2 ? pow_n<R>(lam) : static_tile_A<G>(lam);
+    }
+  }
   __syncthreads();
   float c[LPT][KP];
   mono_read<G, KP>(mono, q, c);
@@ -347,7 +345,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     if constexpr (DYN) A *= lam;
     xr.seal(r);
   }
-  if constexpr (!DYN) A = pow_n<R>(lam_h);
+  if constexpr (!DYN) A = sh_pw[0][q.lt * LPT];
   bool bad = false;
 #pragma unroll
   for (int i = 0; i < LPT; ++i) bad |= Bv[i] != Bv[i];
@@ -383,11 +381,13 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   {
     const int dc = ti.lbd * G::LANES + carry_lane<G>(q);
     const float init_c = (p.ema_init && q.wave < G::NSUB && dc < p.D) ? p.ema_init[(int64_t)ti.b * p.D + dc] : 0.0f;
+    // static lambda: the tile's decay as the look-back recomputes it
+    if constexpr (!DYN) aggA = sh_pw[1][carry_lane<G>(q)];
     const int dlk = ti.lbd * G::LANES + look_lane<G>(q);
-    const float lam_look = DYN ? 0.0f : p.lam[dlk < p.D ? div_hd(dlk, p) : 0];
+    const float a_look = DYN ? 0.0f : sh_pw[1][look_lane<G>(q)];
     LookBack<G, DYN> lbk;
     look_back_issue<G, DYN>(lbk, q, ti, ls);
-    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, lam_look, p.hdr);
+    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, a_look, p.hdr);
   }
 
   float y_after[LPT];
