@@ -6,7 +6,7 @@ import torch
 
 from helpers import assert_close_fp32, inputs, oracle_forward, to_dev
 from oracle import cheby_ema as O
-from orthossm_amd import cheby_ema_forward
+from orthossm_amd import cheby_ema_forward, cheby_ema_ttt
 from orthossm_amd.synthetic import CONFIGS, make_config_inputs
 
 pytestmark = pytest.mark.gpu
@@ -94,6 +94,25 @@ def test_chunked_carry_equals_monolithic(dev, chunk):
     torch.cuda.synchronize()
     assert_close_fp32(torch.cat(outs, 1).cpu(), mono.cpu())
     assert_close_fp32(state.cpu(), fm.cpu(), what="ema_final")
+
+
+@pytest.mark.parametrize("S", [65536, 2 * 65536 + 77])
+def test_long_carry_chain_lambda_near_one(dev, S):
+    """lambda close to 1 keeps the state of a lane alive across hundreds of
+    tiles, so an error in the decay of a full tile (lambda^TILE, recomputed
+    by the look-back under a static lambda) repeats at every tile and adds up
+    (about 1/(1 - lambda^TILE) times over): the carried result must still meet
+    the spec's 1e-5 against the float64 oracle, for the forward and the TTT."""
+    inp = inputs(1, S, 4, 32, 8, seed=S % 1000)
+    inp["lam"] = torch.tensor([0.99999, 0.99995, 0.9999, 0.9995], dtype=torch.float32)
+    d = to_dev(inp, dev)
+    out, fin = cheby_ema_forward(d["x"], d["coeffs"], d["damping"], d["lam"], return_state=True)
+    t_out, _ = cheby_ema_ttt(d["x"], d["coeffs"], d["damping"], d["lam"])
+    torch.cuda.synchronize()
+    want, wfin = oracle_forward(inp)
+    assert_close_fp32(out.cpu(), want)
+    assert_close_fp32(fin.cpu(), wfin, what="ema_final")
+    assert_close_fp32(t_out.cpu(), want, what="TTT out")
 
 
 @pytest.mark.parametrize("g_shape", ["BSH", "SH"])
