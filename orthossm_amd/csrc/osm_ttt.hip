@@ -447,7 +447,6 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     for (int i = 0; i < LPT; ++i) Ar[i] = __builtin_fmaf(bg, Ar[i], sh_al[g][q.lt * LPT + i]);
     Br *= bg;
   }
-  const float ks = ttt_lane_scale<DYN>(p, a.h);
   float* part = p.partials + ((size_t)ti.lb * p.n_tiles + ti.tile) * F * kLanes;
   if (q.tg == 0) {
     // Tile map: a[tile start] = al_0 + beta_0 (Ar_0 + Br_0 rho_tile).
@@ -457,6 +456,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
       part[(size_t)(2 * KP + 1) * kLanes + q.lt * LPT + i] = __builtin_fmaf(beta, Ar[i], rg.al[i]);
     }
   }
+  const float ks = ttt_lane_scale<DYN>(p, a.h);
   // Run contributions P + lam_after F (Ar + Br rho_tile), summed over runs;
   // the per-lane scale is applied to the sums.
   const float cB = lam_after * Br;
@@ -485,64 +485,73 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   finish_block(p.hdr, tags.epoch);
 }
 
-// Merge formula, earlier tile/chunk e followed by combined later part c:
+// Merge of the records n-1 .. 0 of one lane (record i at base + i * rstride,
+// fields kLanes apart) for coefficient k, from the sequence end: record e
+// before the merged later part c gives
 //   P = P_c + P_e + Br_c Q_e,  Q = Q_c + Ar_c Q_e,  Ar = Ar_e Ar_c,  Br = Ar_e Br_c + Br_e.
-template <int KP>
-__device__ __forceinline__ void merge_into(float (&acc)[2 * KP + 2], const float* rec, int stride) {
-  const float Ar_c = acc[2 * KP], Br_c = acc[2 * KP + 1];
+// The loads of NB records are issued together.
+template <int KP, int NB>
+__device__ __forceinline__ void merge_lane(const float* base, size_t rstride, int n, int k, float& P, float& Q,
+                                           float& Ar, float& Br) {
+  P = 0.0f, Q = 0.0f, Ar = 1.0f, Br = 0.0f;
+  for (int top = n - 1; top >= 0; top -= NB) {
+    float Pe[NB], Qe[NB], Ae[NB], Be[NB];
 #pragma unroll
-  for (int k = 0; k < KP; ++k) {
-    const float Pe = rec[(size_t)k * stride];
-    const float Qe = rec[(size_t)(KP + k) * stride];
-    acc[k] = acc[k] + __builtin_fmaf(Br_c, Qe, Pe);
-    acc[KP + k] = __builtin_fmaf(Ar_c, Qe, acc[KP + k]);
+    for (int j = 0; j < NB; ++j) {
+      const float* r = base + (size_t)max(top - j, 0) * rstride;
+      Pe[j] = r[(size_t)k * kLanes];
+      Qe[j] = r[(size_t)(KP + k) * kLanes];
+      Ae[j] = r[(size_t)(2 * KP) * kLanes];
+      Be[j] = r[(size_t)(2 * KP + 1) * kLanes];
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      if (top - j >= 0) {
+        P = P + __builtin_fmaf(Br, Qe[j], Pe[j]);
+        Q = __builtin_fmaf(Ar, Qe[j], Q);
+        const float br = __builtin_fmaf(Ae[j], Br, Be[j]);
+        Ar = Ae[j] * Ar;
+        Br = br;
+      }
+    }
   }
-  const float Ar_e = rec[(size_t)(2 * KP) * stride];
-  const float Br_e = rec[(size_t)(2 * KP + 1) * stride];
-  acc[2 * KP] = Ar_e * Ar_c;
-  acc[2 * KP + 1] = __builtin_fmaf(Ar_e, Br_c, Br_e);
 }
 
-// Level 1: each thread merges up to kChunk consecutive tiles of one lane.
+// Level 1: thread (k, lane) merges coefficient k of up to kChunk consecutive
+// tiles of one lane.
 template <int KP>
-__global__ void __launch_bounds__(64) ttt_merge_chunks(const float* partials, float* chunks, int n_tiles,
-                                                       int n_chunks) {
+__global__ void __launch_bounds__(64 * KP) ttt_merge_chunks(const float* partials, float* chunks, int n_tiles,
+                                                            int n_chunks) {
   constexpr int F = n_fields<KP>();
-  const int chunk = blockIdx.x, lb = blockIdx.y, l = threadIdx.x;
-  float acc[F];
-#pragma unroll
-  for (int v = 0; v < F; ++v) acc[v] = 0.0f;
-  acc[2 * KP] = 1.0f;  // identity map
+  const int chunk = blockIdx.x, lb = blockIdx.y, l = threadIdx.x % kLanes, k = threadIdx.x / kLanes;
   const int first = chunk * kChunk;
-  const int last = min(first + kChunk, n_tiles) - 1;
-  for (int t = last; t >= first; --t)
-    merge_into<KP>(acc, partials + ((size_t)lb * n_tiles + t) * F * kLanes + l, kLanes);
+  const int n = min(first + kChunk, n_tiles) - first;
+  float P, Q, Ar, Br;
+  merge_lane<KP, kChunk>(partials + ((size_t)lb * n_tiles + first) * F * kLanes + l, (size_t)F * kLanes, n, k, P, Q,
+                         Ar, Br);
   float* dst = chunks + ((size_t)lb * n_chunks + chunk) * F * kLanes + l;
-#pragma unroll
-  for (int v = 0; v < F; ++v) dst[(size_t)v * kLanes] = acc[v];
+  dst[(size_t)k * kLanes] = P;
+  dst[(size_t)(KP + k) * kLanes] = Q;
+  if (k == 0) {
+    dst[(size_t)(2 * KP) * kLanes] = Ar;
+    dst[(size_t)(2 * KP + 1) * kLanes] = Br;
+  }
 }
 
 // Level 2: merge the chunks of each lane from the sequence end (rho = 0) and
-// write grad[b,h,k,j] = G_k / (k+1)^2.
+// write grad[b,h,k,j] = G_k / (k+1)^2; thread (k, lane).
 template <int KP>
-__global__ void __launch_bounds__(64) ttt_finalize(const float* chunks, float* grad, int n_chunks, int n_lbd, int D,
-                                                   int hd, int H, int K) {
+__global__ void __launch_bounds__(64 * KP) ttt_finalize(const float* chunks, float* grad, int n_chunks, int n_lbd,
+                                                        int D, int hd, int H, int K) {
   constexpr int F = n_fields<KP>();
-  const int lb = blockIdx.x, l = threadIdx.x;
-  float acc[F];
-#pragma unroll
-  for (int v = 0; v < F; ++v) acc[v] = 0.0f;
-  acc[2 * KP] = 1.0f;
-  for (int c = n_chunks - 1; c >= 0; --c)
-    merge_into<KP>(acc, chunks + ((size_t)lb * n_chunks + c) * F * kLanes + l, kLanes);
+  const int lb = blockIdx.x, l = threadIdx.x % kLanes, k = threadIdx.x / kLanes;
+  float P, Q, Ar, Br;
+  merge_lane<KP, 8>(chunks + (size_t)lb * n_chunks * F * kLanes + l, (size_t)F * kLanes, n_chunks, k, P, Q, Ar, Br);
   const int b = lb / n_lbd;
   const int d = (lb - b * n_lbd) * kLanes + l;
-  if (d >= D) return;
+  if (d >= D || k >= K) return;
   const int h = d / hd, j = d - h * hd;
-  float* gdst = grad + (((size_t)b * H + h) * K) * hd + j;
-#pragma unroll
-  for (int k = 0; k < KP; ++k)
-    if (k < K) gdst[(size_t)k * hd] = acc[k] / (float)((k + 1) * (k + 1));
+  grad[(((size_t)b * H + h) * K + k) * hd + j] = P / (float)((k + 1) * (k + 1));
 }
 
 template <class G, bool DYN, bool SOFT, typename XT, typename OT, int KP>
@@ -553,12 +562,12 @@ hipError_t launch_all(const FwdParams& p, float* grad, hipStream_t stream) {
   if (e != hipSuccess) return e;
   const int n_chunks = (p.n_tiles + kChunk - 1) / kChunk;
   float* chunks = p.partials + (size_t)p.n_lb * p.n_tiles * n_fields<KP>() * kLanes;
-  hipLaunchKernelGGL((ttt_merge_chunks<KP>), dim3(n_chunks, p.n_lb), dim3(64), 0, stream, p.partials, chunks,
+  hipLaunchKernelGGL((ttt_merge_chunks<KP>), dim3(n_chunks, p.n_lb), dim3(64 * KP), 0, stream, p.partials, chunks,
                      p.n_tiles, n_chunks);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((ttt_finalize<KP>), dim3(p.n_lb), dim3(64), 0, stream, chunks, grad, n_chunks, p.n_lbd, p.D,
-                     p.hd, p.H, p.K);
+  hipLaunchKernelGGL((ttt_finalize<KP>), dim3(p.n_lb), dim3(64 * KP), 0, stream, chunks, grad, n_chunks, p.n_lbd,
+                     p.D, p.hd, p.H, p.K);
   return hipGetLastError();
 }
 
