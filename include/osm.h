@@ -97,6 +97,13 @@ typedef enum osm_status {
                                       everywhere (NaN where x is NaN), as the
                                       full path's backward (sdpc_kernel.py:2505),
                                       instead of 0 where |x| < 1e-7 or NaN */
+#define OSM_FLAG_TIMING_JITTER 0x8 /* test aid, no counterpart in the reference:
+                                      every workgroup sleeps a pseudo-random
+                                      0-13 us (hash of its index and the launch)
+                                      before it publishes to the look-back and
+                                      before it combines the words it read, to
+                                      perturb the order in which tiles finish;
+                                      results are unchanged, bit for bit */
 
 /* TTT target y */
 typedef enum osm_ttt_target { OSM_TARGET_X = 0, OSM_TARGET_SOFTSIGN = 1 } osm_ttt_target;

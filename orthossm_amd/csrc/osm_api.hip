@@ -63,7 +63,8 @@ int check_args(const osm_cheby_args* a, Geometry* geo, int op, bool shapes_only 
   if (!a) return fail(OSM_E_ARG, "args is NULL");
   if (a->abi_version != OSM_ABI_VERSION)
     return fail(OSM_E_ARG, "abi_version %d does not match library ABI %d", a->abi_version, OSM_ABI_VERSION);
-  const int known = OSM_FLAG_NO_CLAMP | OSM_FLAG_NAN_ZERO_U | (op == OSM_OP_BWD ? OSM_FLAG_FULL_JACOBIAN : 0);
+  const int known = OSM_FLAG_NO_CLAMP | OSM_FLAG_NAN_ZERO_U | OSM_FLAG_TIMING_JITTER |
+                    (op == OSM_OP_BWD ? OSM_FLAG_FULL_JACOBIAN : 0);
   if (a->flags & ~known) return fail(OSM_E_ARG, "unknown flag bits 0x%x", a->flags);
   if (a->B < 0 || a->S < 0) return fail(OSM_E_SHAPE, "B=%lld and S=%lld must be >= 0", (long long)a->B, (long long)a->S);
   if (a->H < 1 || a->hd < 1)
@@ -175,6 +176,7 @@ osm::FwdParams make_params(const osm_cheby_args* a, const Geometry& geo, void* w
   p.lam_max = a->lam_max;
   p.clamp_out = (a->flags & OSM_FLAG_NO_CLAMP) ? 0 : 1;
   p.nan_zero_u = (a->flags & OSM_FLAG_NAN_ZERO_U) ? 1 : 0;
+  p.jitter = (a->flags & OSM_FLAG_TIMING_JITTER) ? 1 : 0;
   return p;
 }
 

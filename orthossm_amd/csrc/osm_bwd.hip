@@ -285,6 +285,7 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
   __builtin_amdgcn_s_setprio(0);
   const LaneSlots ls = lane_slots<G, true>(p.slots, ti, p.n_tiles);
   float pA, pB[1], aggA, aggB;
+  jitter(p.jitter, tags.epoch, 0);
   tile_scan<G, true>(L, qc, ti, tags, A, Bv, pA, pB, aggA, aggB, ls);
   {
     const int dc = ti.lbd * G::LANES + carry_lane<G>(q);
@@ -292,6 +293,7 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
         (bp.grad_state && q.wave < G::NSUB && dc < p.D) ? bp.grad_state[(int64_t)ti.b * p.D + dc] : 0.0f;
     LookBack<G, true> lbk;
     look_back_issue<G, true>(lbk, q, ti, ls);
+    jitter(p.jitter, tags.epoch, 1);
     look_back_finish<G, true>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, 0.0f, p.hdr);
   }
   float v = __builtin_fmaf(pA, L.carry[q.lt], pB[0]);

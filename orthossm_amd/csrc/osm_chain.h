@@ -132,6 +132,21 @@ __device__ __forceinline__ float static_tile_A(float lam) {
   return pow_n<G::TILE>(lam);
 }
 
+// Test aid (OSM_FLAG_TIMING_JITTER): the workgroup sleeps 0..15 x ~0.85 us,
+// a hash of its index, the launch epoch and `site`, so tiles publish and
+// combine in orders the normal schedule rarely produces.  Every wait of the
+// look-back is on a word a predecessor publishes without waiting on later
+// tiles, so a delay only postpones, and results must not change.
+__device__ __forceinline__ void jitter(int on, unsigned epoch, unsigned site) {
+  if (!on) return;
+  unsigned h = (blockIdx.x * 0x9E3779B1u) ^ (epoch * 0x85EBCA77u) ^ (site * 0xC2B2AE3Du);
+  h ^= h >> 15;
+  h *= 0x2C1B3C6Du;
+  h ^= h >> 12;
+  const unsigned n = __builtin_amdgcn_readfirstlane(h & 15u);
+  for (unsigned i = 0; i < n; ++i) __builtin_amdgcn_s_sleep(32);
+}
+
 // Token-group scan.  In: this thread's run aggregate (A, Bv).  Out: (pA, pB)
 // mapping the tile carry to the state before this thread's first token; in
 // waves < NSUB, (aggA, aggB) = the tile aggregate of carry_lane(q), which is

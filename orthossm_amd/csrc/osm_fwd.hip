@@ -204,6 +204,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
 
   const LaneSlots ls = lane_slots<G, DYN>(p.slots, ti, p.n_tiles);
   float pA, pB[LPT], aggA, aggB;
+  jitter(p.jitter, tags.epoch, 0);
   tile_scan<G, DYN>(L, q, ti, tags, A, Bv, pA, pB, aggA, aggB, ls);
   {
     const int dc = ti.lbd * G::LANES + carry_lane<G>(q);
@@ -215,6 +216,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     const float a_look = DYN ? 0.0f : static_tile_A<G>(p.lam[dlk < p.D ? div_hd(dlk, p) : 0]);
     LookBack<G, DYN> lbk;
     look_back_issue<G, DYN>(lbk, q, ti, ls);
+    jitter(p.jitter, tags.epoch, 1);
     look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, a_look, p.hdr);
   }
   finish_complete(p.hdr, tags.epoch, fin_prev);

@@ -137,6 +137,7 @@ struct FwdParams {
   float lam_shift, lam_min, lam_max;
   int clamp_out;
   int nan_zero_u;              // NaN x counts as u = 0 (else z = 0)
+  int jitter;                  // OSM_FLAG_TIMING_JITTER: pseudo-random delays (test aid)
   float ttt_scale;             // 2 / (B*(S-1)*D)
   int ttt_target;
 };

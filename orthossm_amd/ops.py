@@ -40,6 +40,19 @@ def set_fault_check(on: bool) -> bool:
     return old
 
 
+# Test aid: with timing jitter on, the forward, TTT and backward launches
+# carry OSM_FLAG_TIMING_JITTER (every workgroup sleeps a pseudo-random time
+# before it publishes to the look-back); results must not change.
+_timing_jitter = False
+
+
+def set_timing_jitter(on: bool) -> bool:
+    """Turns OSM_FLAG_TIMING_JITTER on or off for later launches; returns the old setting."""
+    global _timing_jitter
+    old, _timing_jitter = _timing_jitter, bool(on)
+    return old
+
+
 def workspace_status(ws: torch.Tensor, *, reset: bool = False, stream: int | None = None) -> tuple[int, int]:
     """(fault word, launch counter) of a workspace, read on ``stream`` (the
     current stream of its device by default) through osm_workspace_status;
@@ -156,7 +169,8 @@ def _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, 
     a.abi_version = nat.ABI_VERSION
     if nan_policy not in ("zero_z", "zero_u"):
         raise ValueError("nan_policy must be 'zero_z' or 'zero_u'")
-    a.flags = (0 if clamp else nat.FLAG_NO_CLAMP) | (nat.FLAG_NAN_ZERO_U if nan_policy == "zero_u" else 0)
+    a.flags = ((0 if clamp else nat.FLAG_NO_CLAMP) | (nat.FLAG_NAN_ZERO_U if nan_policy == "zero_u" else 0) |
+               (nat.FLAG_TIMING_JITTER if _timing_jitter else 0))
     a.B, a.S, a.H, a.hd, a.K = B, S, H, hd, K
     a.x, a.x_dtype, a.x_stride_b, a.x_stride_s = x.data_ptr(), _dtype_code(x.dtype), x.stride(0), x.stride(1)
     a.out_dtype = _dtype_code(odt)

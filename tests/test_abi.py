@@ -90,6 +90,17 @@ def test_workspace_bytes_formula():
     assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 0
 
 
+def test_flag_values_match_the_header():
+    text = open(os.path.join(ROOT, "include", "osm.h")).read()
+    for name in ("NO_CLAMP", "NAN_ZERO_U", "FULL_JACOBIAN", "TIMING_JITTER"):
+        m = re.search(rf"#define OSM_FLAG_{name} (0x[0-9a-fA-F]+)", text)
+        assert m and int(m.group(1), 16) == getattr(nat, f"FLAG_{name}"), name
+    lib = nat.load()
+    # the timing-jitter test aid is accepted by the forward, TTT and backward
+    for op in (nat.OP_FWD, nat.OP_TTT, nat.OP_BWD):
+        assert lib.osm_workspace_bytes(ctypes.byref(_args(flags=nat.FLAG_TIMING_JITTER)), op) > 0
+
+
 def test_coefficient_limits_per_entry_point():
     lib = nat.load()
     for K in (9, 16):
