@@ -60,6 +60,26 @@ __device__ __forceinline__ void v10_softsign(float xb, float& absu, float& sgn) 
   sgn = xs >= 0.0f ? 1.0f : -1.0f;
 }
 
+// Sum over the runs of a wave (lanes l, l + LW, l + 2 LW, ...) in every
+// lane, as the butterfly v += v[lane ^ o] for o = LW, 2 LW, .. 32, with
+// cross-lane moves that stay in the VALU: a DPP row rotate by 8 (lane ^ 8
+// inside each 16-lane row) and the gfx950 row swaps, whose two results for
+// (v, v) are (row 0, row 0, row 2, row 2) and (row 1, row 1, row 3, row 3)
+// (v_permlane16_swap) and (lower half twice) and (upper half twice)
+// (v_permlane32_swap).  Each step adds a lane's value and its partner's, as
+// the butterfly does (the same sums, in either operand order).
+template <int LW>
+__device__ __forceinline__ float sum_runs(float v) {
+  typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+  static_assert(LW == 8 || LW == 16, "8 or 16 lanes per workgroup");
+  if constexpr (LW == 8)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+  const u32x2v a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a.x) + __uint_as_float(a.y);
+  const u32x2v b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b.x) + __uint_as_float(b.y);
+}
+
 template <int LW>
 struct V10Lds {
   static constexpr int NW = kV10Groups * LW / 64;   // waves per workgroup
@@ -328,9 +348,7 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
     // wave, then the waves in order), then Lion.
 #pragma unroll
     for (int k = 0; k < KP; ++k) {
-      float v = gc[k];
-#pragma unroll
-      for (int o = LW; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+      const float v = sum_runs<LW>(gc[k]);
       if (gw == 0) L.ws[wave][k][l] = v;
     }
     __syncthreads();
