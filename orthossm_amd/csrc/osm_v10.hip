@@ -248,16 +248,21 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
             ta[4 * q4] = va.x; ta[4 * q4 + 1] = va.y; ta[4 * q4 + 2] = va.z; ta[4 * q4 + 3] = va.w;
             tb[4 * q4] = vb.x; tb[4 * q4 + 1] = vb.y; tb[4 * q4 + 2] = vb.z; tb[4 * q4 + 3] = vb.w;
           }
-          float ye = 0.0f, yo = 0.0f;
+          // the series at both table points, then one interpolation (linear
+          // in the table: the value of interpolating each T_k, up to rounding)
+          float ae = 0.0f, ao = 0.0f, be = 0.0f, bo = 0.0f;
 #pragma unroll
           for (int k = 0; k < KP; ++k) {
-            const float it = __builtin_fmaf(fr, tb[k] - ta[k], ta[k]);
-            if (k & 1)
-              yo = __builtin_fmaf(c[k], it, yo);
-            else
-              ye = __builtin_fmaf(c[k], it, ye);
+            if (k & 1) {
+              ao = __builtin_fmaf(c[k], ta[k], ao);
+              bo = __builtin_fmaf(c[k], tb[k], bo);
+            } else {
+              ae = __builtin_fmaf(c[k], ta[k], ae);
+              be = __builtin_fmaf(c[k], tb[k], be);
+            }
           }
-          y = __builtin_fmaf(sgn, yo, ye);
+          const float ya = __builtin_fmaf(sgn, ao, ae), yb = __builtin_fmaf(sgn, bo, be);
+          y = __builtin_fmaf(fr, yb - ya, ya);
         } else {
           const float uu = u[r], u2 = uu + uu;
           const float c3 = c[3], c2 = c[2];
