@@ -21,6 +21,8 @@
 // LDS; the proxy-gradient sums are reduced over the runs in a fixed order,
 // and (lanes x K) threads apply Lion and publish the next chunk's
 // coefficients through LDS.
+#include <type_traits>
+
 #include "osm_tile.h"
 
 namespace osm {
@@ -227,64 +229,76 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
 
       float u[R + 1], w[R];
       float A = 1.0f, Bv = 0.0f;
+      // A block whose runs are all inside the chunk skips the per-token
+      // checks (each loop below comes in both versions; the choice is the
+      // same for the whole workgroup): only the last token of a run may
+      // lack its pair (the chunk's last token), checked once per run.
+      const bool full = (blk + 1) * kBlockTok <= len;
+      auto pass1 = [&](auto full_c) {
+        constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
-      for (int r = 0; r <= R; ++r) {
-        const float xb = to_bf16_value<XT>(xcur[r]);
-        float absu, sgn;
-        v10_softsign(xb, absu, sgn);
-        u[r] = sgn * absu;
-        if (r == R) break;   // the row after the run: u only
-        float y;
-        if constexpr (LUT) {
-          const float fidx = absu * 255.0f;
-          const int i0 = min((int)fidx, 254);
-          const float fr = __builtin_fminf(__builtin_fmaxf(fidx - (float)i0, 0.0f), 1.0f);
-          float ta[KP], tb[KP];
-          const f32x4* ra = reinterpret_cast<const f32x4*>(&L.lut[i0][0]);
-          const f32x4* rb = reinterpret_cast<const f32x4*>(&L.lut[i0 + 1][0]);
+        for (int r = 0; r <= R; ++r) {
+          const float xb = to_bf16_value<XT>(xcur[r]);
+          float absu, sgn;
+          v10_softsign(xb, absu, sgn);
+          u[r] = sgn * absu;
+          if (r == R) break;   // the row after the run: u only
+          float y;
+          if constexpr (LUT) {
+            const float fidx = absu * 255.0f;
+            const int i0 = min((int)fidx, 254);
+            const float fr = __builtin_fminf(__builtin_fmaxf(fidx - (float)i0, 0.0f), 1.0f);
+            float ta[KP], tb[KP];
+            const f32x4* ra = reinterpret_cast<const f32x4*>(&L.lut[i0][0]);
+            const f32x4* rb = reinterpret_cast<const f32x4*>(&L.lut[i0 + 1][0]);
 #pragma unroll
-          for (int q4 = 0; q4 < KP / 4; ++q4) {
-            const f32x4 va = ra[q4], vb = rb[q4];
-            ta[4 * q4] = va.x; ta[4 * q4 + 1] = va.y; ta[4 * q4 + 2] = va.z; ta[4 * q4 + 3] = va.w;
-            tb[4 * q4] = vb.x; tb[4 * q4 + 1] = vb.y; tb[4 * q4 + 2] = vb.z; tb[4 * q4 + 3] = vb.w;
-          }
-          // the series at both table points, then one interpolation (linear
-          // in the table: the value of interpolating each T_k, up to rounding)
-          float ae = 0.0f, ao = 0.0f, be = 0.0f, bo = 0.0f;
-#pragma unroll
-          for (int k = 0; k < KP; ++k) {
-            if (k & 1) {
-              ao = __builtin_fmaf(c[k], ta[k], ao);
-              bo = __builtin_fmaf(c[k], tb[k], bo);
-            } else {
-              ae = __builtin_fmaf(c[k], ta[k], ae);
-              be = __builtin_fmaf(c[k], tb[k], be);
+            for (int q4 = 0; q4 < KP / 4; ++q4) {
+              const f32x4 va = ra[q4], vb = rb[q4];
+              ta[4 * q4] = va.x; ta[4 * q4 + 1] = va.y; ta[4 * q4 + 2] = va.z; ta[4 * q4 + 3] = va.w;
+              tb[4 * q4] = vb.x; tb[4 * q4 + 1] = vb.y; tb[4 * q4 + 2] = vb.z; tb[4 * q4 + 3] = vb.w;
             }
+            // the series at both table points, then one interpolation (linear
+            // in the table: the value of interpolating each T_k, up to rounding)
+            float ae = 0.0f, ao = 0.0f, be = 0.0f, bo = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KP; ++k) {
+              if (k & 1) {
+                ao = __builtin_fmaf(c[k], ta[k], ao);
+                bo = __builtin_fmaf(c[k], tb[k], bo);
+              } else {
+                ae = __builtin_fmaf(c[k], ta[k], ae);
+                be = __builtin_fmaf(c[k], tb[k], be);
+              }
+            }
+            const float ya = __builtin_fmaf(sgn, ao, ae), yb = __builtin_fmaf(sgn, bo, be);
+            y = __builtin_fmaf(fr, yb - ya, ya);
+          } else {
+            const float uu = u[r], u2 = uu + uu;
+            const float c3 = c[3], c2 = c[2];
+            const float b2 = __builtin_fmaf(u2, c3, c2);
+            const float b1 = __builtin_fmaf(u2, b2, c[1]) - c3;
+            y = __builtin_fmaf(uu, b1, c[0]) - b2;
           }
-          const float ya = __builtin_fmaf(sgn, ao, ae), yb = __builtin_fmaf(sgn, bo, be);
-          y = __builtin_fmaf(fr, yb - ya, ya);
-        } else {
-          const float uu = u[r], u2 = uu + uu;
-          const float c3 = c[3], c2 = c[2];
-          const float b2 = __builtin_fmaf(u2, c3, c2);
-          const float b1 = __builtin_fmaf(u2, b2, c[1]) - c3;
-          y = __builtin_fmaf(uu, b1, c[0]) - b2;
+          const float yc = __builtin_amdgcn_fmed3f(gamma * y, -4.0f, 4.0f);
+          const float e2 = __builtin_amdgcn_exp2f(2.0f * kLog2e * yc);
+          float z = (e2 - 1.0f) * __builtin_amdgcn_rcpf(e2 + 1.0f);
+          z = xb == xb ? z : 0.0f;
+          w[r] = one_m * z;
+          if (FULL || r < n_valid) {
+            Bv = __builtin_fmaf(mu, Bv, w[r]);
+            A *= mu;
+          }
+          if (p.z_save && (FULL || r < n_valid)) {
+            const float zz[1] = {z};
+            BufVec<__bf16, 1>::store(zr, lane_ok ? (uint32_t)(g * R) * z_row + (uint32_t)(d * 2) : kOffOOB,
+                                     (uint32_t)r * z_row, zz);
+          }
         }
-        const float yc = __builtin_amdgcn_fmed3f(gamma * y, -4.0f, 4.0f);
-        const float e2 = __builtin_amdgcn_exp2f(2.0f * kLog2e * yc);
-        float z = (e2 - 1.0f) * __builtin_amdgcn_rcpf(e2 + 1.0f);
-        z = xb == xb ? z : 0.0f;
-        w[r] = one_m * z;
-        if (r < n_valid) {
-          Bv = __builtin_fmaf(mu, Bv, w[r]);
-          A *= mu;
-        }
-        if (p.z_save && r < n_valid) {
-          const float zz[1] = {z};
-          BufVec<__bf16, 1>::store(zr, lane_ok ? (uint32_t)(g * R) * z_row + (uint32_t)(d * 2) : kOffOOB,
-                                   (uint32_t)r * z_row, zz);
-        }
-      }
+      };
+      if (full)
+        pass1(std::true_type{});
+      else
+        pass1(std::false_type{});
       // Compose the runs: inclusive scan inside the wave (later map applied
       // after earlier: A = A_l A_e, B = A_l B_e + B_l), then the waves.
       float iA = A, iB = Bv;
@@ -311,30 +325,37 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
       s = __builtin_fmaf(eA, s, eB);
       // Replay, store bf16(s), proxy gradient.
       const uint32_t ovo = lane_ok ? (uint32_t)(g * R) * o_row + (uint32_t)(d * 4) : kOffOOB;
+      auto replay = [&](auto full_c) {
+        constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if (r < n_valid) {
-          s = __builtin_fmaf(mu, s, w[r]);
-          const float so = __builtin_amdgcn_fmed3f(s, -1.0f, 1.0f);
-          const float ov[1] = {(float)(__bf16)so};
-          BufVec<float, 1>::store(orr, ovo, (uint32_t)r * o_row, ov);
-          if (r0 + r + 1 < len) {
-            const float err = u[r + 1] - so;
-            const float gv = err * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-3.0f * kLog2e * __builtin_fabsf(err)));
-            const float uu = u[r], u2 = uu + uu;
-            gc[0] += gv;
-            if constexpr (KP > 1) gc[1] = __builtin_fmaf(gv, uu, gc[1]);
-            float tm2 = 1.0f, tm1 = uu;
+        for (int r = 0; r < R; ++r) {
+          if (FULL || r < n_valid) {
+            s = __builtin_fmaf(mu, s, w[r]);
+            const float so = __builtin_amdgcn_fmed3f(s, -1.0f, 1.0f);
+            const float ov[1] = {(float)(__bf16)so};
+            BufVec<float, 1>::store(orr, ovo, (uint32_t)r * o_row, ov);
+            if ((FULL && r + 1 < R) || r0 + r + 1 < len) {
+              const float err = u[r + 1] - so;
+              const float gv = err * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-3.0f * kLog2e * __builtin_fabsf(err)));
+              const float uu = u[r], u2 = uu + uu;
+              gc[0] += gv;
+              if constexpr (KP > 1) gc[1] = __builtin_fmaf(gv, uu, gc[1]);
+              float tm2 = 1.0f, tm1 = uu;
 #pragma unroll
-            for (int k = 2; k < KP; ++k) {
-              const float tk = __builtin_fmaf(u2, tm1, -tm2);
-              gc[k] = __builtin_fmaf(gv, tk, gc[k]);
-              tm2 = tm1;
-              tm1 = tk;
+              for (int k = 2; k < KP; ++k) {
+                const float tk = __builtin_fmaf(u2, tm1, -tm2);
+                gc[k] = __builtin_fmaf(gv, tk, gc[k]);
+                tm2 = tm1;
+                tm1 = tk;
+              }
             }
           }
         }
-      }
+      };
+      if (full)
+        replay(std::true_type{});
+      else
+        replay(std::false_type{});
       if (len > kBlockTok) {
         // The next block of this chunk starts from this block's end state
         // (a one-block chunk has no next block: the carry restarts at 0).
