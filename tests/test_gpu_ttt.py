@@ -92,6 +92,27 @@ def test_ttt_nan_inputs(dev, nan_policy):
     assert O.rel_err(g[ok], G[ok]) <= 1e-3
 
 
+@pytest.mark.parametrize("lams", [(0.0, 1.0, 0.5, 0.999), (1.02, 0.9, 1.0, 0.3)])
+def test_ttt_edge_lambdas(dev, lams):
+    """lambda = 1 (no decay: the gradient scale 1/(1-lambda) is never formed,
+    the derivative is 0), lambda = 0 (no memory) and lambda > 1 (s leaves
+    [-1, 1] even from a zero start, so runs must take the path that clamps and
+    masks), with an initial state outside [-1, 1] on some lanes."""
+    H = len(lams)
+    inp = inputs(2, 1500, H, 16, 8, seed=47)
+    inp["lam"] = torch.tensor(lams, dtype=torch.float32)
+    init = torch.rand(2, H * 16, generator=torch.Generator().manual_seed(48)) * 3.0 - 1.5
+    out, grad, fin = run(inp, dev, ema_init=init.to(dev), return_state=True)
+    G, want, wfin = oracle_ttt(inp, ema_init=init.numpy())
+    assert_close_fp32(out.cpu(), want)
+    assert_close_fp32(fin.cpu(), wfin, what="ema_final")
+    assert_grad(grad, G)
+    g = grad.cpu().numpy()
+    for h, lam in enumerate(lams):
+        if lam == 1.0:
+            assert not np.any(g[:, h]), f"head {h} (lambda = 1): the gradient is 0"
+
+
 def test_ttt_forward_matches_forward_kernel(dev):
     inp = to_dev(inputs(2, 5000, 8, 64, 8, seed=41, dynamic=True), dev)
     o1 = cheby_ema_forward(inp["x"], inp["coeffs"], inp["damping"], inp["lam"], g=inp["g"])
