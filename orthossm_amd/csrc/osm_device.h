@@ -320,23 +320,41 @@ __device__ __forceinline__ float clenshaw(float u, const float* c) {
 
 // Monomial form of a Chebyshev series.  T_k has only powers u^j with
 // j = k - 2i, so coefficient j of sum_{k<8} c_k T_k(u) is
-//     sum_{i<4} kChebMono[j][i] * c_{j+2i}
+//     sum_{i<4} cheb_mono(j, i) * c_{j+2i}
 // with the textbook expansions T_0 = 1, T_1 = u, T_2 = 2u^2 - 1,
 // T_3 = 4u^3 - 3u, T_4 = 8u^4 - 8u^2 + 1, T_5 = 16u^5 - 20u^3 + 5u,
 // T_6 = 32u^6 - 48u^4 + 18u^2 - 1, T_7 = 64u^7 - 112u^5 + 56u^3 - 7u.
 // Evaluating the series as Horner on these coefficients takes K-1 FMAs per
 // point against 2(K-1) operations for Clenshaw; in fp32 both errors stay
-// ~1e-6 for |c_k| = O(1), |u| <= 1 at K = 8.
-__device__ const float kChebMono[8][4] = {
-    {1.0f, -1.0f, 1.0f, -1.0f},     // u^0 from T_0, T_2, T_4, T_6
-    {1.0f, -3.0f, 5.0f, -7.0f},     // u^1 from T_1, T_3, T_5, T_7
-    {2.0f, -8.0f, 18.0f, 0.0f},     // u^2 from T_2, T_4, T_6
-    {4.0f, -20.0f, 56.0f, 0.0f},    // u^3 from T_3, T_5, T_7
-    {8.0f, -48.0f, 0.0f, 0.0f},     // u^4 from T_4, T_6
-    {16.0f, -112.0f, 0.0f, 0.0f},   // u^5 from T_5, T_7
-    {32.0f, 0.0f, 0.0f, 0.0f},      // u^6 from T_6
-    {64.0f, 0.0f, 0.0f, 0.0f},      // u^7 from T_7
-};
+// ~1e-6 for |c_k| = O(1), |u| <= 1 at K = 8.  A constexpr function rather
+// than a table in device memory: with j a template argument the factors are
+// instruction constants (a table indexed at run time is a memory load on the
+// path to every tile's first arithmetic).
+__host__ __device__ constexpr float cheb_mono(int j, int i) {
+  switch (j * 4 + i) {
+    case 0: return 1.0f;   case 1: return -1.0f;   case 2: return 1.0f;   case 3: return -1.0f;  // u^0: T_0,T_2,T_4,T_6
+    case 4: return 1.0f;   case 5: return -3.0f;   case 6: return 5.0f;   case 7: return -7.0f;  // u^1: T_1,T_3,T_5,T_7
+    case 8: return 2.0f;   case 9: return -8.0f;   case 10: return 18.0f;                        // u^2: T_2,T_4,T_6
+    case 12: return 4.0f;  case 13: return -20.0f; case 14: return 56.0f;                        // u^3: T_3,T_5,T_7
+    case 16: return 8.0f;  case 17: return -48.0f;                                               // u^4: T_4,T_6
+    case 20: return 16.0f; case 21: return -112.0f;                                              // u^5: T_5,T_7
+    case 24: return 32.0f;                                                                       // u^6: T_6
+    case 28: return 64.0f;                                                                       // u^7: T_7
+    default: return 0.0f;
+  }
+}
+
+// Monomial coefficient J (unscaled) from the Chebyshev coefficients
+// c_{J+2i}, i < 4, in float64.  Terms whose factor is 0 are left out: they
+// pair only with c_k for k >= 8, which the callers load as 0.
+template <int J>
+__device__ __forceinline__ double mono_coef(const float (&cm)[4]) {
+  double acc = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (cheb_mono(J, i) != 0.0f) acc = __builtin_fma((double)cheb_mono(J, i), (double)cm[i], acc);
+  return acc;
+}
 
 // Horner evaluation of sum_j a[j] u^j.
 template <int KP>

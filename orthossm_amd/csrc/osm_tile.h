@@ -66,7 +66,7 @@ __device__ __forceinline__ uint32_t next_off(uint32_t off, uint32_t step) {
 // Clenshaw, see series()).  The work is split in units (coefficient j,
 // 64-lane sub-block sb); wave w takes units w, w + WAVES, ... and forms
 // coefficient j of its 64 lanes from <= 4 Chebyshev coefficients
-// (kChebMono) in float64 (monomial form) or scales c_j (Chebyshev form);
+// (cheb_mono) in float64 (monomial form) or scales c_j (Chebyshev form);
 // results are shared through LDS.
 // Split in three steps so the caller can issue these loads before its bulk
 // loads (the conversion then waits only for them) and convert after issuing
@@ -124,8 +124,17 @@ __device__ __forceinline__ void mono_store(const MonoLoad<KP, G>& m, const Threa
       if constexpr (KP > kMonoMaxK) {
         acc = (double)m.cm[n][0];
       } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc = __builtin_fma((double)kChebMono[j][i], (double)m.cm[n][i], acc);
+        // j is wave-uniform: a scalar branch to the constants of coefficient j
+        switch (j) {
+          case 0: acc = mono_coef<0>(m.cm[n]); break;
+          case 1: acc = mono_coef<1>(m.cm[n]); break;
+          case 2: acc = mono_coef<2>(m.cm[n]); break;
+          case 3: acc = mono_coef<3>(m.cm[n]); break;
+          case 4: acc = mono_coef<4>(m.cm[n]); break;
+          case 5: acc = mono_coef<5>(m.cm[n]); break;
+          case 6: acc = mono_coef<6>(m.cm[n]); break;
+          default: acc = mono_coef<7>(m.cm[n]); break;
+        }
       }
       mono[j][(u % G::NSUB) * kLanes + q.wl] = (float)(acc * (double)m.kap[n]);
     }
