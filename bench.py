@@ -387,6 +387,27 @@ def main():
     torch.cuda.synchronize()
     copy_ms = c0.elapsed_time(c1) / n_copy
     copy_gbs = 2 * xs[0].numel() * xs[0].element_size() / (copy_ms * 1e-3) / 1e9
+    # Chunked workloads launch one kernel per chunk: a copy of one chunk's
+    # bytes (consecutive slices of the buffers, as the chunks are) is the
+    # like-for-like reference for a launch of that size.
+    chunk_copy_gbs = None
+    if cfg.chunk:
+        n_sl = cfg.S // cfg.chunk
+
+        def copy_chunk(i):
+            t0 = (i % n_sl) * cfg.chunk
+            outs[i % args.sets][:, t0:t0 + cfg.chunk].copy_(xs[(i + 1) % args.sets][:, t0:t0 + cfg.chunk])
+
+        for i in range(n_sl):
+            copy_chunk(i)
+        torch.cuda.synchronize()
+        c0.record(stream)
+        for i in range(10 * n_sl):
+            copy_chunk(i)
+        c1.record(stream)
+        torch.cuda.synchronize()
+        chunk_bytes = 2 * cfg.B * cfg.chunk * cfg.D * xs[0].element_size()
+        chunk_copy_gbs = chunk_bytes / (c0.elapsed_time(c1) / (10 * n_sl) * 1e-3) / 1e9
     tokens = cfg.B * cfg.S
     algo = algorithmic_bytes(cfg)
     launches = cfg.S // cfg.chunk if cfg.chunk else 1
@@ -436,6 +457,9 @@ def main():
             "frac_of_copy": achieved_gbs / copy_gbs,
         },
     }
+    if chunk_copy_gbs is not None:
+        res["roofline"]["copy_gbs_one_chunk"] = chunk_copy_gbs
+        res["roofline"]["frac_of_chunk_copy"] = achieved_gbs / chunk_copy_gbs
     if args.calibrate_copy:
         for i in range(5):
             outs[i % args.sets].copy_(xs[(i + 1) % args.sets])
