@@ -162,8 +162,9 @@ def measured_traffic(workload: str):
         return None
 
 
-# The auxiliary kernels of a step (tile merges / reductions).
-AUX_KERNELS = ("ttt_merge", "ttt_finalize", "bwd_reduce")
+# The auxiliary kernels of a step (the TTT's per-launch coefficient table,
+# tile merges / reductions).
+AUX_KERNELS = ("ttt_mono_prep", "ttt_merge", "ttt_finalize", "bwd_reduce")
 
 
 def main_kernel(cfg) -> str:

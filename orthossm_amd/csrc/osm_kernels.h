@@ -124,6 +124,7 @@ struct FwdParams {
   unsigned long long* slots;   // look-back words [n_lb][n_tiles][LANES][words]
   unsigned* hdr;               // WsHeader
   float* partials;             // TTT per-tile partials (TTT kernels only)
+  float* mono_tab;             // TTT: scaled monomial coefficients [n_lb][KP][64], formed once per launch
   int64_t x_sb, x_ss, o_sb, o_ss;
   int64_t c_sb, c_sh, c_sk;
   int64_t g_sb, g_ss, g_sh;

@@ -273,7 +273,10 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     return;
   }
   const TileAddr a = tile_addr<G, DYN, XT, OT>(p, q, ti);
-  const auto ml = mono_issue<KP, G>(p, q, ti, a);
+  // This wave's monomial coefficient (wave w holds coefficient w of the 64
+  // lanes), formed once per launch by ttt_mono_prep; loaded before x.
+  static_assert(G::NSUB == 1 && KP <= G::WAVES, "one coefficient per wave");
+  const float mono_w = q.wave < KP ? p.mono_tab[((size_t)ti.lb * KP + q.wave) * kLanes + q.wl] : 0.0f;
 
   // x rows of the run (raw), g (dynamic lambda), and for the tile's last run
   // the row after the tile (its target y and lambda).
@@ -305,7 +308,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     }
   }
 
-  mono_store<KP, G>(ml, q, mono);
+  if (q.wave < KP) mono[q.wave][q.wl] = mono_w;
   if constexpr (!DYN) {
     // lambda^R and lambda^TILE of each lane, by the last two waves
     if (q.wave >= G::WAVES - 2) {
@@ -489,6 +492,41 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   finish_block(p.hdr, tags.epoch);
 }
 
+// The scaled monomial coefficients of every lane-block, as the forward forms
+// them per tile (mono_issue / mono_store): coefficient j of lane l from
+// c_{j+2i} in float64 with the factors cheb_mono(j, i), times 2 log2(e)
+// damping_h, rounded once.  Thread (j, lane) of block lb; lanes >= D get 0.
+template <int KP>
+__global__ void __launch_bounds__(64 * KP) ttt_mono_prep(const FwdParams p, float* tab) {
+  const int lb = blockIdx.x, j = threadIdx.x / kLanes, l = threadIdx.x % kLanes;
+  const int b = lb / p.n_lbd;
+  const int d = (lb - b * p.n_lbd) * kLanes + l;
+  float cm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float kap = 0.0f;
+  if (d < p.D) {
+    const int h = div_hd(d, p);
+    const float* c = p.coeffs + (int64_t)b * p.c_sb + (int64_t)h * p.c_sh + (d - h * p.hd);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = j + 2 * i;
+      cm[i] = k < p.K ? c[(int64_t)k * p.c_sk] : 0.0f;
+    }
+    kap = kTwoLog2e * p.damping[h];
+  }
+  double acc = 0.0;
+  switch (j) {
+    case 0: acc = mono_coef<0>(cm); break;
+    case 1: acc = mono_coef<1>(cm); break;
+    case 2: acc = mono_coef<2>(cm); break;
+    case 3: acc = mono_coef<3>(cm); break;
+    case 4: acc = mono_coef<4>(cm); break;
+    case 5: acc = mono_coef<5>(cm); break;
+    case 6: acc = mono_coef<6>(cm); break;
+    default: acc = mono_coef<7>(cm); break;
+  }
+  tab[((size_t)lb * KP + j) * kLanes + l] = (float)(acc * (double)kap);
+}
+
 // Merge of the records n-1 .. 0 of one lane (record i at base + i * rstride,
 // fields kLanes apart) for coefficient k, from the sequence end: record e
 // before the merged later part c gives
@@ -559,13 +597,18 @@ __global__ void __launch_bounds__(64 * KP) ttt_finalize(const float* chunks, flo
 }
 
 template <class G, bool DYN, bool SOFT, typename XT, typename OT, int KP>
-hipError_t launch_all(const FwdParams& p, float* grad, hipStream_t stream) {
-  const unsigned grid = (unsigned)p.n_lb_pad * (unsigned)p.n_tiles;
-  hipLaunchKernelGGL((cheby_ema_ttt_kernel<G, DYN, SOFT, XT, OT, KP>), dim3(grid), dim3(G::THREADS), 0, stream, p);
+hipError_t launch_all(const FwdParams& p0, float* grad, hipStream_t stream) {
+  const int n_chunks = (p0.n_tiles + kChunk - 1) / kChunk;
+  float* chunks = p0.partials + (size_t)p0.n_lb * p0.n_tiles * n_fields<KP>() * kLanes;
+  FwdParams p = p0;
+  p.mono_tab = chunks + (size_t)p.n_lb * n_chunks * n_fields<KP>() * kLanes;
+  hipLaunchKernelGGL((ttt_mono_prep<KP>), dim3(p.n_lb), dim3(64 * KP), 0, stream, p, p.mono_tab);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int n_chunks = (p.n_tiles + kChunk - 1) / kChunk;
-  float* chunks = p.partials + (size_t)p.n_lb * p.n_tiles * n_fields<KP>() * kLanes;
+  const unsigned grid = (unsigned)p.n_lb_pad * (unsigned)p.n_tiles;
+  hipLaunchKernelGGL((cheby_ema_ttt_kernel<G, DYN, SOFT, XT, OT, KP>), dim3(grid), dim3(G::THREADS), 0, stream, p);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((ttt_merge_chunks<KP>), dim3(n_chunks, p.n_lb), dim3(64 * KP), 0, stream, p.partials, chunks,
                      p.n_tiles, n_chunks);
   e = hipGetLastError();
@@ -608,7 +651,8 @@ size_t ttt_workspace_bytes(int n_lb, int n_tiles, bool dyn, int K) {
   const size_t F = 2 * kpad + 2;
   const size_t n_chunks = (n_tiles + kChunk - 1) / kChunk;
   const size_t slots = (fwd_workspace_bytes(n_lb, n_tiles, TttTile::LANES, dyn) + 255) / 256 * 256;
-  return slots + ((size_t)n_lb * n_tiles + (size_t)n_lb * n_chunks) * F * kLanes * sizeof(float);
+  // per-tile partials, per-chunk merges, the monomial table
+  return slots + (((size_t)n_lb * n_tiles + (size_t)n_lb * n_chunks) * F + (size_t)n_lb * kpad) * kLanes * sizeof(float);
 }
 
 hipError_t launch_ttt(const FwdParams& p, float* grad, int x_dtype, int out_dtype, bool dyn, int tile, int kpad,
