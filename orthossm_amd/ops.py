@@ -93,6 +93,18 @@ def _after_launch(ws: torch.Tensor, stream: int, what: str) -> None:
                                                 f"launch counter {epoch}); the results of that launch are invalid")
 
 
+# The raw handle of a device's current stream: torch's C accessor when this
+# torch has it (a tenth of the host time of building a Stream object, which
+# shows on launches of small inputs), else the public API.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _current_stream(dev: torch.device) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
 def _workspace(device: torch.device, stream: int, nbytes: int, op: int) -> torch.Tensor:
     """Zero-initialised workspace reused per (device, stream, entry point).
     Calls on one stream are ordered, so they never overlap on a workspace;
@@ -110,8 +122,12 @@ def _workspace(device: torch.device, stream: int, nbytes: int, op: int) -> torch
 
 
 def _as_param(v, H: int, device, name: str) -> torch.Tensor:
-    t = v if isinstance(v, torch.Tensor) else torch.as_tensor(v, dtype=torch.float32)
-    t = t.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    if (isinstance(v, torch.Tensor) and v.dtype is torch.float32 and v.dim() == 1 and v.is_contiguous()
+            and v.device == device):
+        t = v   # already in the kernel's form: no conversion calls (host time per launch)
+    else:
+        t = v if isinstance(v, torch.Tensor) else torch.as_tensor(v, dtype=torch.float32)
+        t = t.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
     if t.numel() != H:
         raise ValueError(f"{name} must have H={H} entries, got {t.numel()}")
     return t
@@ -142,7 +158,8 @@ def _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, 
     Bc, H, K, hd = coeffs.shape
     if Bc != B or H * hd != D:
         raise ValueError(f"coeffs {tuple(coeffs.shape)} does not match x {tuple(x.shape)}")
-    c = coeffs.to(device=dev, dtype=torch.float32)
+    c = coeffs if (coeffs.dtype is torch.float32 and coeffs.device == dev) else coeffs.to(device=dev,
+                                                                                            dtype=torch.float32)
     if c.stride(3) != 1:
         c = c.contiguous()
     damp = _as_param(damping, H, dev, "damping")
@@ -209,7 +226,7 @@ def cheby_ema_forward(x: torch.Tensor, coeffs: torch.Tensor, damping: Sequence[f
                             out_dtype, out, nan_policy)
     dev = out.device
     ema_final = _state_buffer(a, dev, return_state, state_out)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _current_stream(dev)
     nbytes = lib.osm_workspace_bytes(ctypes.byref(a), 0)
     if nbytes == 0:
         nat.check(_rc_from_error(lib, a, 0))
@@ -245,7 +262,7 @@ def cheby_ema_ttt(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, *, g: tor
         _check_dest(grad_out, (a.B, a.H, a.K, a.hd), dev, "grad_out")
         grad = grad_out
     ema_final = _state_buffer(a, dev, return_state, state_out)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _current_stream(dev)
     nbytes = lib.osm_workspace_bytes(ctypes.byref(a), 1)
     if nbytes == 0:
         nat.check(_rc_from_error(lib, a, 1))
@@ -325,7 +342,7 @@ def cheby_ema_backward(x: torch.Tensor, coeffs: torch.Tensor, damping, lam, out:
         bw.z_saved, bw.z_stride_b, bw.z_stride_s = z_saved.data_ptr(), z_saved.stride(0), z_saved.stride(1)
     if full_jacobian:
         a.flags |= nat.FLAG_FULL_JACOBIAN
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _current_stream(dev)
     nbytes = lib.osm_workspace_bytes(ctypes.byref(a), nat.OP_BWD)
     if nbytes == 0:
         nat.check(lib.osm_cheby_ema_bwd(ctypes.byref(a), ctypes.byref(bw), None, 0, None))
@@ -525,7 +542,7 @@ def v10_chunked_ttt(x: torch.Tensor, coeffs: torch.Tensor, momentum: torch.Tenso
     if z is not None:
         a.z_save, a.z_stride_b, a.z_stride_s = z.data_ptr(), z.stride(0), z.stride(1)
         a.coeff_hist = hist.data_ptr()
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _current_stream(dev)
     nat.check(lib.osm_v10_chunked_ttt(ctypes.byref(a), ctypes.c_void_p(stream)))
     keep = (x, c, m, gate, dyn, mu_dev)  # noqa: F841  (alive until the launch is queued)
     if Kfull > K:

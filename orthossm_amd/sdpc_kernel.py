@@ -133,6 +133,40 @@ def v10_damping(n_heads: int, device=None) -> torch.Tensor:
     return 0.98 - 0.06 * h / n_heads
 
 
+# The fast path's per-head damping and lambda tensors, built once per
+# (device, heads) and (device, heads, momentum) instead of on every call (a
+# call with small inputs otherwise spends most of its host time building
+# them).  Entries are never dropped (a cached tensor may still be read by a
+# launch on another stream); past _CONST_CACHE_MAX entries new values are
+# built per call instead.
+_const_lock = threading.Lock()
+_const_cache: dict = {}
+_CONST_CACHE_MAX = 64
+
+
+def _fast_constants(n_heads: int, device: torch.device, ema_momentum):
+    """(damping [H], lam [H]) fp32 on ``device`` for the fast path; a tensor
+    ``ema_momentum`` (on the device, not read back) is expanded per call."""
+    dev = torch.device(device)
+    dkey = ("damping", dev, n_heads)
+    if isinstance(ema_momentum, torch.Tensor):
+        lkey = None
+    else:
+        lkey = ("lam", dev, n_heads, float(ema_momentum))
+    with _const_lock:
+        damping = _const_cache.get(dkey)
+        lam = _const_cache.get(lkey) if lkey is not None else None
+    if damping is None:
+        damping = v10_damping(n_heads, dev)
+    if lam is None:
+        lam = head_momentum(ema_momentum, n_heads, dev)
+    with _const_lock:
+        for key, val in ((dkey, damping), (lkey, lam)):
+            if key is not None and len(_const_cache) < _CONST_CACHE_MAX:
+                _const_cache.setdefault(key, val)
+    return damping, lam
+
+
 def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_momentum=0.9,
                         lion_beta1=0.9, lion_beta2=0.99, lion_wd=0.01, chunk_size=256, use_bf16=False,
                         gate_global=None, dynamic_lambda=None, use_lut=True, seq_threshold=384,
@@ -166,8 +200,7 @@ def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_m
         # take up to 16 (more than 8 by Clenshaw).
         raise ValueError(f"the fast path supports at most {MAX_FAST_TERMS} Chebyshev coefficients, "
                          f"got {coeffs.shape[2]}")
-    damping = v10_damping(H, x.device)
-    lam = head_momentum(ema_momentum, H, x.device)
+    damping, lam = _fast_constants(H, x.device, ema_momentum)
     if torch.is_grad_enabled() and (x.requires_grad or coeffs.requires_grad):
         out = cheby_ema(x, coeffs, damping, lam, out_dtype=torch.float32, nan_policy="zero_u")
     else:
