@@ -90,6 +90,29 @@ def test_workspace_bytes_formula():
     assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 0
 
 
+def test_ttt_workspace_bytes_formula():
+    """TTT: the forward's header and look-back words for 192-token tiles of
+    64 lanes (one word per lane, static lambda), 256-byte aligned, then per
+    lane 2K+2 floats per tile (the tile records) and per chunk of 16 tiles
+    (their merges), then K floats per lane (the per-launch monomial
+    coefficients), with K padded to 4 or 8."""
+    lib = nat.load()
+    a = _args()
+    n_lb, n_tiles = 4 * 8, -(-16384 // 192)
+    n_chunks = -(-n_tiles // 16)
+
+    def want(kpad, words):
+        slots = 2048 + n_lb * n_tiles * 64 * 8 * words
+        slots = -(-slots // 256) * 256
+        return slots + ((n_lb * n_tiles + n_lb * n_chunks) * (2 * kpad + 2) + n_lb * kpad) * 64 * 4
+
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 1) == want(8, 1)
+    a.K = 3
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 1) == want(4, 1)
+    a.K, a.g = 8, 0x10000
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 1) == want(8, 2)
+
+
 def test_flag_values_match_the_header():
     text = open(os.path.join(ROOT, "include", "osm.h")).read()
     for name in ("NO_CLAMP", "NAN_ZERO_U", "FULL_JACOBIAN", "TIMING_JITTER"):
