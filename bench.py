@@ -1,11 +1,15 @@
 """Benchmark of the fused Cheby-RKV forward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload W] [--no-others]
 
 Default workload: BASELINE configs[1] ("headline"): B=4, S=16384, D=512
 (H=8, hd=64), K=8, fp32, static per-head lambda.  One step = one pass of
 the fused operator over one batch held in HBM.  Inputs rotate over 4
 buffer sets (>1 GB) so the 256 MB Infinity Cache cannot serve them.
+Without --workload the run then times every other workload of
+synthetic.CONFIGS the same way (100 warm-up and 100 timed steps each, on
+inputs drawn on the device, two buffer sets where x exceeds 256 MB) and
+reports them under ``other_workloads``; --workload W times W only.
 
 Prints ONE JSON line (rank 0).  The timed region is exactly K steps
 back to back between two HIP events on the stream the kernels run on.
@@ -37,7 +41,7 @@ sys.path.insert(0, ROOT)
 
 from orthossm_amd import cheby_ema_backward, cheby_ema_forward, cheby_ema_ttt  # noqa: E402
 from orthossm_amd.ops import v10_chunked_ttt  # noqa: E402
-from orthossm_amd.synthetic import CONFIGS, make_config_inputs  # noqa: E402
+from orthossm_amd.synthetic import CONFIGS, baseline_damping, baseline_lambda, make_config_inputs  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "Clenshaw+EMA tokens/s and HBM GB/s (% of peak) at B=4 S=16K D=512, 1 GPU"
@@ -267,6 +271,135 @@ def pmc_summary(read_path: str, write_path: str, workload: str) -> dict:
     return out
 
 
+def device_inputs(cfg, dev, seed: int = 0):
+    """The distributions of synthetic.make_inputs drawn on the device (fast
+    for the large configs; values differ from the CPU draw, timings do not
+    depend on them)."""
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    k = torch.arange(cfg.K, dtype=torch.float32, device=dev).view(1, 1, cfg.K, 1)
+    return {
+        "x": torch.randn(cfg.B, cfg.S, cfg.D, device=dev, generator=gen).to(cfg.dtype),
+        "coeffs": torch.randn(cfg.B, cfg.H, cfg.K, cfg.hd, device=dev, generator=gen) / (k + 1.0),
+        "damping": baseline_damping(cfg.H).to(dev),
+        "lam": baseline_lambda(cfg.H).to(dev),
+        "g": (torch.rand(cfg.B, cfg.S, cfg.H, device=dev, generator=gen) * 2.0 - 1.0) if cfg.dynamic else None,
+    }
+
+
+class Workload:
+    """Device buffers of one workload (inputs and outputs rotating over
+    ``sets`` buffer sets) and its step: one pass of the operator over one
+    batch (one launch per chunk for chunked workloads)."""
+
+    def __init__(self, cfg, dev, sets: int, inp: dict):
+        self.cfg, self.sets = cfg, sets
+        x0 = inp["x"]
+        self.c, self.damp, self.lam, self.g = inp["coeffs"], inp["damping"], inp["lam"], inp["g"]
+        self.xs = [x0] + [x0.clone() for _ in range(sets - 1)]
+        self.outs = [torch.empty_like(x0) for _ in range(sets)]
+        # EMA state: every launch reads ema_init and writes ema_final; chunks
+        # ping-pong between two state buffers.
+        self.state0 = torch.zeros(cfg.B, cfg.D, device=dev)
+        self.states = [torch.empty_like(self.state0), torch.empty_like(self.state0)]
+        self.grad = torch.empty(cfg.B, cfg.H, cfg.K, cfg.hd, device=dev) if (cfg.ttt or cfg.bwd) else None
+        if cfg.bwd:
+            # Saved forward outputs and dL/dout per buffer set; dL/dx goes to gxs.
+            gen = torch.Generator(device=dev).manual_seed(1)
+            for x, out in zip(self.xs, self.outs):
+                cheby_ema_forward(x, self.c, self.damp, self.lam, g=self.g, out=out)
+            self.gos = [torch.randn(x0.shape, device=dev, generator=gen) for _ in range(sets)]
+            self.gxs = [torch.empty_like(x0) for _ in range(sets)]
+            torch.cuda.synchronize()
+        self.mom = torch.zeros_like(self.c) if cfg.v10 else None
+
+    def step(self, i):
+        cfg, c, damp, lam, g = self.cfg, self.c, self.damp, self.lam, self.g
+        x, out = self.xs[i % self.sets], self.outs[i % self.sets]
+        if cfg.v10:
+            v10_chunked_ttt(x, c, self.mom, n_heads=cfg.H, chunk_size=cfg.v10)
+        elif cfg.bwd:
+            cheby_ema_backward(x, c, damp, lam, out, self.gos[i % self.sets], g=g, grad_state=self.state0,
+                               grad_x_out=self.gxs[i % self.sets], grad_coeffs_out=self.grad,
+                               grad_init_out=self.states[0])
+        elif cfg.ttt:
+            cheby_ema_ttt(x, c, damp, lam, g=g, out=out, ema_init=self.state0, state_out=self.states[0],
+                          grad_out=self.grad)
+        elif cfg.chunk:
+            prev = self.state0
+            for n, t0 in enumerate(range(0, cfg.S, cfg.chunk)):
+                cheby_ema_forward(x[:, t0:t0 + cfg.chunk], c, damp, lam, ema_init=prev,
+                                  out=out[:, t0:t0 + cfg.chunk], state_out=self.states[n % 2])
+                prev = self.states[n % 2]
+        else:
+            cheby_ema_forward(x, c, damp, lam, g=g, out=out, ema_init=self.state0, state_out=self.states[0])
+
+
+def time_steps(step, steps: int, warmup: int, stream) -> float:
+    """Milliseconds per step: ``warmup`` untimed steps, then exactly
+    ``steps`` steps back to back between two events on the launch stream,
+    nothing else enqueued in between."""
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for i in range(steps):
+        step(i)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    return t_start.elapsed_time(t_end) / steps
+
+
+def launch_figures(cfg, ms_per_step: float) -> dict:
+    """Tokens/s and the HBM roofline of the average launch of a step."""
+    launches = cfg.S // cfg.chunk if cfg.chunk else 1
+    algo_launch = algorithmic_bytes(cfg) / launches
+    kernel_ms = ms_per_step / launches
+    gbs = algo_launch / (kernel_ms * 1e-3) / 1e9
+    return {"value": cfg.B * cfg.S / (ms_per_step * 1e-3), "achieved": gbs, "frac": gbs / HBM_PEAK_GBS,
+            "algorithmic_bytes": algo_launch, "launches_per_step": launches, "kernel_ms_mean": kernel_ms}
+
+
+def other_workloads(skip: str, dev, stream, steps: int, warmup: int) -> dict:
+    """The other BASELINE workloads, each timed as the main one is (its own
+    warm-up, then ``steps`` steps between two events), on inputs drawn on
+    the device, at most two buffer sets above 256 MB of x."""
+    res = {}
+    for name, cfg in CONFIGS.items():
+        if name in (skip, "cpu_ref"):
+            continue
+        esz = 2 if cfg.dtype == torch.bfloat16 else 4
+        sets = 4 if cfg.B * cfg.S * cfg.D * esz <= (256 << 20) else 2
+        W = Workload(cfg, dev, sets, device_inputs(cfg, dev))
+        ms = time_steps(W.step, steps, warmup, stream)
+        f = launch_figures(cfg, ms)
+        res[name] = {
+            "ms_per_step": ms, "value": f["value"], "unit": "tokens/s",
+            "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp32",
+            "roofline": {"bound": "hbm", "achieved": f["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": f["frac"], "traffic": measured_traffic(name),
+                         "algorithmic_bytes": f["algorithmic_bytes"],
+                         "launches_per_step": f["launches_per_step"], "kernel_ms_mean": f["kernel_ms_mean"]},
+            "steps": steps, "warmup": warmup, "sets": sets,
+            "config": workload_label(cfg),
+        }
+        del W
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return res
+
+
+def workload_label(cfg) -> str:
+    return (f"BASELINE {cfg.name}: B={cfg.B} S={cfg.S} D={cfg.D} H={cfg.H} hd={cfg.hd} K={cfg.K} "
+            f"{'bf16' if cfg.dtype == torch.bfloat16 else 'fp32'}"
+            f"{' dynamic-lambda' if cfg.dynamic else ''}{' +TTT-grad' if cfg.ttt else ''}"
+            f"{' backward (dL/dx, dL/dc, dL/d ema_init)' if cfg.bwd else ''}"
+            f"{f' full path: chunks of {cfg.v10} with Lion, LUT series' if cfg.v10 else ''}"
+            f"{f' as {cfg.S // cfg.chunk} chunks with carry' if cfg.chunk else ''}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -275,7 +408,10 @@ def main():
     # and 500 timed steps (a few seconds at most for any workload).
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=500)
-    ap.add_argument("--workload", default="headline", choices=sorted(CONFIGS))
+    ap.add_argument("--workload", default=None, choices=sorted(CONFIGS),
+                    help="time this workload only (default: the headline, then each other workload briefly)")
+    ap.add_argument("--no-others", action="store_true",
+                    help="without --workload: time the headline only")
     ap.add_argument("--sets", type=int, default=4, help="rotating input/output buffer sets")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -287,6 +423,8 @@ def main():
                          "READ_COUNTERS / WRITE_COUNTERS) into HBM bytes per launch for W, stored in "
                          "profiles/hbm_traffic.json")
     args = ap.parse_args()
+    others = args.workload is None and not args.no_others and not args.calibrate_copy
+    args.workload = args.workload or "headline"
     if args.pmc_summary:
         print(json.dumps({args.workload: pmc_summary(*args.pmc_summary, args.workload)}, indent=1))
         return
@@ -302,67 +440,11 @@ def main():
     cfg = CONFIGS[args.workload]
     dev = torch.device("cuda", 0)
     inp = make_config_inputs(cfg)
-    x0 = inp["x"].to(dev)
-    c = inp["coeffs"].to(dev)
-    damp = inp["damping"].to(dev)
-    lam = inp["lam"].to(dev)
-    g = inp["g"].to(dev) if inp["g"] is not None else None
-    xs = [x0] + [x0.clone() for _ in range(args.sets - 1)]
-    outs = [torch.empty_like(x0) for _ in range(args.sets)]
+    W = Workload(cfg, dev, args.sets, {k: (v.to(dev) if v is not None else None) for k, v in inp.items()})
     del inp
-
-    # EMA state: every launch reads ema_init and writes ema_final; chunks
-    # ping-pong between two state buffers.
-    state0 = torch.zeros(cfg.B, cfg.D, device=dev)
-    states = [torch.empty_like(state0), torch.empty_like(state0)]
-    grad = torch.empty(cfg.B, cfg.H, cfg.K, cfg.hd, device=dev) if (cfg.ttt or cfg.bwd) else None
-    if cfg.bwd:
-        # Saved forward outputs and dL/dout per buffer set; dL/dx goes to gxs.
-        gen = torch.Generator(device=dev).manual_seed(1)
-        for x, out in zip(xs, outs):
-            cheby_ema_forward(x, c, damp, lam, g=g, out=out)
-        gos = [torch.randn(x0.shape, device=dev, generator=gen) for _ in range(args.sets)]
-        gxs = [torch.empty_like(x0) for _ in range(args.sets)]
-        torch.cuda.synchronize()
-
-    mom = torch.zeros_like(c) if cfg.v10 else None
-
-    def step(i):
-        x, out = xs[i % args.sets], outs[i % args.sets]
-        if cfg.v10:
-            v10_chunked_ttt(x, c, mom, n_heads=cfg.H, chunk_size=cfg.v10)
-        elif cfg.bwd:
-            cheby_ema_backward(x, c, damp, lam, out, gos[i % args.sets], g=g, grad_state=state0,
-                               grad_x_out=gxs[i % args.sets], grad_coeffs_out=grad, grad_init_out=states[0])
-        elif cfg.ttt:
-            cheby_ema_ttt(x, c, damp, lam, g=g, out=out, ema_init=state0, state_out=states[0], grad_out=grad)
-        elif cfg.chunk:
-            prev = state0
-            for n, t0 in enumerate(range(0, cfg.S, cfg.chunk)):
-                cheby_ema_forward(x[:, t0:t0 + cfg.chunk], c, damp, lam, ema_init=prev,
-                                  out=out[:, t0:t0 + cfg.chunk], state_out=states[n % 2])
-                prev = states[n % 2]
-        else:
-            cheby_ema_forward(x, c, damp, lam, g=g, out=out, ema_init=state0, state_out=states[0])
-
+    xs, outs, step = W.xs, W.outs, W.step
     stream = torch.cuda.current_stream(dev)
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
-    # Timed region: exactly K steps between two events on the launch stream,
-    # nothing else enqueued in between, so the average step is the average
-    # duration of the fused operator's launch(es) back to back.
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_start.record(stream)
-    for i in range(args.steps):
-        step(i)
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    total_ms = t_start.elapsed_time(t_end)
-    ms_per_step = total_ms / args.steps
+    ms_per_step = time_steps(step, args.steps, args.warmup, stream)
     # Spread of single steps (a second, separately timed pass with an event
     # pair around every step; each pair adds a few microseconds of dispatch
     # overhead, so these read slightly high).
@@ -409,18 +491,14 @@ def main():
         torch.cuda.synchronize()
         chunk_bytes = 2 * cfg.B * cfg.chunk * cfg.D * xs[0].element_size()
         chunk_copy_gbs = chunk_bytes / (c0.elapsed_time(c1) / (10 * n_sl) * 1e-3) / 1e9
-    tokens = cfg.B * cfg.S
-    algo = algorithmic_bytes(cfg)
-    launches = cfg.S // cfg.chunk if cfg.chunk else 1
-    mean_kernel_ms = ms_per_step / launches
-    algo_launch = algo / launches
-    achieved_gbs = algo_launch / (mean_kernel_ms * 1e-3) / 1e9
+    f = launch_figures(cfg, ms_per_step)
+    achieved_gbs = f["achieved"]
 
     res = {
         "metric": METRIC if args.workload == "headline" else
         f"Clenshaw+EMA {'backward ' if cfg.bwd else ''}{'full path (online TTT + Lion) ' if cfg.v10 else ''}"
         f"tokens/s, workload {cfg.name}",
-        "value": tokens / (ms_per_step * 1e-3),
+        "value": f["value"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -432,12 +510,7 @@ def main():
         "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp32",
         "data": "synthetic (seeded N(0,1) inputs, c_k ~ N(0,1/(k+1)^2))",
         "config": {
-            "workload": f"BASELINE {cfg.name}: B={cfg.B} S={cfg.S} D={cfg.D} H={cfg.H} hd={cfg.hd} K={cfg.K} "
-                        f"{'bf16' if cfg.dtype == torch.bfloat16 else 'fp32'}"
-                        f"{' dynamic-lambda' if cfg.dynamic else ''}{' +TTT-grad' if cfg.ttt else ''}"
-                        f"{' backward (dL/dx, dL/dc, dL/d ema_init)' if cfg.bwd else ''}"
-                        f"{f' full path: chunks of {cfg.v10} with Lion, LUT series' if cfg.v10 else ''}"
-                        f"{f' as {cfg.S // cfg.chunk} chunks with carry' if cfg.chunk else ''}",
+            "workload": workload_label(cfg),
             "B": cfg.B, "S": cfg.S, "D": cfg.D, "H": cfg.H, "K": cfg.K,
             "parallelism": "single GPU",
         },
@@ -446,11 +519,11 @@ def main():
             "achieved": achieved_gbs,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": achieved_gbs / HBM_PEAK_GBS,
+            "frac": f["frac"],
             "traffic": measured_traffic(args.workload),
-            "algorithmic_bytes": algo_launch,
-            "launches_per_step": launches,
-            "kernel_ms_mean": mean_kernel_ms,
+            "algorithmic_bytes": f["algorithmic_bytes"],
+            "launches_per_step": f["launches_per_step"],
+            "kernel_ms_mean": f["kernel_ms_mean"],
             "step_ms_evented_p10": per[len(per) // 10],
             "step_ms_evented_median": per[len(per) // 2],
             "step_ms_evented_p90": per[(9 * len(per)) // 10],
@@ -466,6 +539,13 @@ def main():
             outs[i % args.sets].copy_(xs[(i + 1) % args.sets])
         torch.cuda.synchronize()
         res["copy_calibration_bytes_each_way"] = xs[0].numel() * xs[0].element_size()
+    if others:
+        # Each other BASELINE workload timed in the same run (100 warm-up
+        # and 100 timed steps each), so that one run records all of them.
+        del W, xs, outs, step
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        res["other_workloads"] = other_workloads(args.workload, dev, stream, steps=100, warmup=100)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(cfg)
     print(json.dumps(res), flush=True)
