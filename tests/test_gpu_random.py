@@ -188,3 +188,39 @@ def test_random_full_path(dev, seed):
                       gate_global=None if gate is None else gate.numpy(),
                       dynamic_lambda=None if dyn is None else dyn.numpy(), **kw)
     compare_v10(out, cn, mn, want)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_full_path_gradients(dev, seed):
+    """dL/dx (and dL/dc for one-chunk sequences, the only case where the
+    chunk loop lets it flow) of the differentiable drop-in against the
+    oracle's backward of the full path on the GPU forward's saved tensors."""
+    from orthossm_amd import apply_cheby_rkv_v10
+
+    r = np.random.default_rng(5000 + seed)
+    H = int(r.choice((1, 2, 4, 8)))
+    hd = int(r.choice((4, 8, 16, 24, 32, 64)))
+    B = int(r.integers(1, 4))
+    K = int(r.integers(1, 9))
+    chunk = int(r.choice((64, 100, 256, 512)))
+    S = int(r.integers(2, 1200))
+    print(f"B={B} S={S} H={H} hd={hd} K={K} chunk={chunk}", flush=True)
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, S, H * hd, generator=gen)
+    c = torch.randn(B, H, K, hd, generator=gen) / torch.arange(1, K + 1).view(1, 1, K, 1)
+    m = torch.randn(B, H, K, hd, generator=gen) * 0.01
+    go = torch.randn(B, S, H * hd, generator=gen)
+    xd = x.to(dev).requires_grad_(True)
+    cd = c.to(dev).requires_grad_(True)
+    out, _, _ = apply_cheby_rkv_v10(xd, cd, m.to(dev), n_heads=H, chunk_size=chunk, seq_threshold=0)
+    (out * go.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    _, _, _, z, hist = v10_chunked_ttt(x.to(dev), c.to(dev), m.to(dev), n_heads=H, chunk_size=chunk,
+                                       save_for_backward=True)
+    wx, wc = V.v10_backward(x.numpy(), out.detach().cpu().numpy(), z.float().cpu().numpy(), hist.cpu().numpy(),
+                            go.numpy(), n_heads=H, ema_momentum=0.9, chunk=chunk)
+    assert_close_grad(xd.grad.cpu(), wx, what="grad_x")
+    if S <= chunk:
+        assert_close_grad(cd.grad.cpu(), wc, what="grad_coeffs")
+    else:
+        assert cd.grad is None
