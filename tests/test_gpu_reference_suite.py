@@ -1,0 +1,124 @@
+"""The path-level checks of the reference's own V10 suite, run against this
+drop-in: test_v10.py T2 (shapes), T3 (fast path below seq_threshold leaves
+the coefficients alone), T4 and T5 (the full path above it updates them),
+T6 (Lion keeps two state tensors), T7 (LUT and 4-term Clenshaw series
+agree, cosine > 0.99), T8 (gradients through the op finite and non-zero),
+T9 (B=4 finite), T13 and T14 (degree 4 and 8 run; timings printed), with
+the coefficients drawn by init_chebyshev_coefficients as there
+(test_v10.py:63-241, 330-385).  Its model-level checks (T1, T10-T12,
+T15-T17: imports, the layer bus, the full model, the local refiner) are
+outside this path.  Where it is cheap the outputs are also compared with
+the CPU oracle (oracle/v10_full.py)."""
+import time
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import compare_v10
+from oracle import v10_full as V
+from orthossm_amd import sdpc_kernel as K10
+
+pytestmark = pytest.mark.gpu
+
+B, S, D, NH = 2, 512, 64, 8
+HD = D // NH
+DEG = 4   # the reference's V10 default
+
+
+def _coef(dev, b=B, deg=DEG, seed=0):
+    torch.manual_seed(seed)
+    return K10.init_chebyshev_coefficients(b, NH, deg, HD, dev)
+
+
+def test_t2_forward_shapes(dev):
+    x = torch.randn(B, S, D, generator=torch.Generator().manual_seed(2)).to(dev)
+    coef = _coef(dev)
+    mom = torch.zeros_like(coef)
+    out, cn, mn = K10.apply_cheby_rkv_v10(x, coef, mom, n_heads=NH, ema_momentum=0.9)
+    assert out.shape == x.shape and cn.shape == coef.shape and mn.shape == mom.shape
+
+
+def test_t3_fast_path_keeps_coefficients(dev):
+    x = torch.randn(2, 128, D, generator=torch.Generator().manual_seed(3)).to(dev)
+    coef = _coef(dev, seed=3)
+    mom = torch.zeros_like(coef)
+    out, cn, mn = K10.apply_cheby_rkv_v10(x, coef, mom, n_heads=NH, ema_momentum=0.9, seq_threshold=384)
+    torch.cuda.synchronize()
+    assert out.shape == x.shape
+    assert torch.allclose(cn, coef, atol=1e-6)
+
+
+@pytest.mark.parametrize("seq", [512, 1024])
+def test_t4_t5_full_path_updates_coefficients(dev, seq):
+    x = torch.randn(2, seq, D, generator=torch.Generator().manual_seed(seq)).to(dev)
+    coef = _coef(dev, seed=seq)
+    mom = torch.zeros_like(coef)
+    out, cn, mn = K10.apply_cheby_rkv_v10(x, coef, mom, n_heads=NH, ema_momentum=0.9, seq_threshold=384)
+    torch.cuda.synchronize()
+    assert out.shape == x.shape
+    assert not torch.allclose(cn, coef, atol=1e-6)
+    # and the same values as the CPU restatement
+    compare_v10(out, cn, mn, V.v10_full(x.cpu().numpy(), coef.double().cpu().numpy(),
+                                        mom.double().cpu().numpy(), n_heads=NH, ema_momentum=0.9))
+
+
+def test_t6_lion_state_is_two_tensors(dev):
+    x = torch.randn(2, 600, D, generator=torch.Generator().manual_seed(6)).to(dev)
+    coef = _coef(dev, seed=6)
+    res = K10.apply_cheby_rkv_v10(x, coef, torch.zeros_like(coef), n_heads=NH, seq_threshold=0)
+    assert len(res) == 3                      # out, coefficients, momentum: no second moment
+    state = res[1].numel() + res[2].numel()
+    assert (1 - state / (3 * coef.numel())) * 100 > 30
+
+
+def test_t7_lut_and_clenshaw_agree(dev):
+    x = torch.randn(2, 512, D, generator=torch.Generator().manual_seed(7)).to(dev)
+    coef = _coef(dev, seed=7)
+    outs = []
+    for lut in (True, False):
+        out, cn, mn = K10.apply_cheby_rkv_v10(x, coef.clone(), torch.zeros_like(coef), n_heads=NH, ema_momentum=0.9,
+                                              use_lut=lut, seq_threshold=0)
+        torch.cuda.synchronize()
+        compare_v10(out, cn, mn, V.v10_full(x.cpu().numpy(), coef.double().cpu().numpy(),
+                                            np.zeros(coef.shape), n_heads=NH, ema_momentum=0.9, use_lut=lut))
+        outs.append(out)
+    cos = torch.nn.functional.cosine_similarity(outs[0].reshape(1, -1), outs[1].reshape(1, -1)).item()
+    print(f"T7 cosine {cos:.5f}", flush=True)
+    assert cos > 0.99
+
+
+def test_t8_gradients_finite_and_nonzero(dev):
+    x = torch.randn(2, 512, D, generator=torch.Generator().manual_seed(8)).to(dev).requires_grad_(True)
+    coef = _coef(dev, seed=8)
+    out, _, _ = K10.apply_cheby_rkv_v10(x, coef, torch.zeros_like(coef), n_heads=NH, ema_momentum=0.9,
+                                        seq_threshold=0)
+    out.sum().backward()
+    torch.cuda.synchronize()
+    assert x.grad is not None and torch.isfinite(x.grad).all() and x.grad.abs().max() > 0
+
+
+def test_t9_multi_batch_finite(dev):
+    x = torch.randn(4, 512, D, generator=torch.Generator().manual_seed(9)).to(dev)
+    coef = _coef(dev, b=4, seed=9)
+    out, _, _ = K10.apply_cheby_rkv_v10(x, coef, torch.zeros_like(coef), n_heads=NH, ema_momentum=0.9,
+                                        seq_threshold=0)
+    assert torch.isfinite(out).all()
+
+
+def test_t13_t14_degree_four_and_eight_timed(dev):
+    x = torch.randn(2, 1024, D, generator=torch.Generator().manual_seed(13)).to(dev)
+    for deg in (4, 8):
+        coef = _coef(dev, deg=deg, seed=deg)
+        mom = torch.zeros_like(coef)
+        for _ in range(3):
+            K10.apply_cheby_rkv_v10(x, coef.clone(), mom.clone(), n_heads=NH, ema_momentum=0.9, seq_threshold=0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(20):
+            out, _, _ = K10.apply_cheby_rkv_v10(x, coef.clone(), mom.clone(), n_heads=NH, ema_momentum=0.9,
+                                                seq_threshold=0)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / 20 * 1e3
+        print(f"degree {deg}: {ms:.3f} ms per call (B=2 S=1024 D=64, host included)", flush=True)
+        assert torch.isfinite(out).all()
