@@ -1,14 +1,17 @@
-"""The path-level checks of the reference's own V10 suite, run against this
-drop-in: test_v10.py T2 (shapes), T3 (fast path below seq_threshold leaves
-the coefficients alone), T4 and T5 (the full path above it updates them),
+"""The path-level checks of the reference's own suites, run against this
+drop-in.  From test_v10.py: T2 (shapes), T3 (fast path below
+seq_threshold leaves the coefficients alone), T4 and T5 (the full path above it updates them),
 T6 (Lion keeps two state tensors), T7 (LUT and 4-term Clenshaw series
 agree, cosine > 0.99), T8 (gradients through the op finite and non-zero),
 T9 (B=4 finite), T13 and T14 (degree 4 and 8 run; timings printed), with
 the coefficients drawn by init_chebyshev_coefficients as there
 (test_v10.py:63-241, 330-385).  Its model-level checks (T1, T10-T12,
 T15-T17: imports, the layer bus, the full model, the local refiner) are
-outside this path.  Where it is cheap the outputs are also compared with
-the CPU oracle (oracle/v10_full.py)."""
+outside this path.  From precision_tests.py: P1 (a one-chunk call equals
+the plain series + EMA), P2 (bf16-rounded coefficients move the output by
+<= 1.5%), P4 (one-chunk gradients finite) and P5 (<= 3 ms per forward).
+Where it is cheap the outputs are also compared with the CPU oracle
+(oracle/v10_full.py)."""
 import time
 
 import numpy as np
@@ -122,3 +125,74 @@ def test_t13_t14_degree_four_and_eight_timed(dev):
         ms = (time.perf_counter() - t0) / 20 * 1e3
         print(f"degree {deg}: {ms:.3f} ms per call (B=2 S=1024 D=64, host included)", flush=True)
         assert torch.isfinite(out).all()
+
+
+# The path-level checks of the reference's precision_tests.py (P1, P2, P4,
+# P5; precision_tests.py:29-199).  P3 tests the local refiner (outside this
+# path).
+
+def test_p1_single_chunk_equals_the_plain_series_and_ema(dev):
+    """One chunk (S=256 < chunk_size=512): out is the LUT series + EMA with
+    the starting coefficients (the reference compares its megakernel with
+    its pure Clenshaw+EMA kernel: cosine >= 0.99, mean error <= 1% of the
+    mean magnitude), and Lion has updated the coefficients."""
+    b, s, nh, deg = 2, 256, 8, 4
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(b, s, D, generator=gen).to(dev)
+    c0 = torch.randn(b, nh, deg, D // nh, generator=gen).to(dev)
+    m0 = torch.zeros_like(c0)
+    out, cn, _ = K10.apply_cheby_rkv_v10(x, c0.clone(), m0.clone(), n_heads=nh, use_lut=True, seq_threshold=0,
+                                         chunk_size=512)
+    torch.cuda.synchronize()
+    # plain series + EMA, no Lion: the oracle's chunk with a zero learning rate
+    want, _, _ = V.v10_full(x.cpu().numpy(), c0.double().cpu().numpy(), np.zeros(c0.shape), n_heads=nh,
+                            base_lr=0.0, chunk_size=512)
+    o = out.float().cpu().flatten()
+    w = torch.from_numpy(want).float().flatten()
+    cos = torch.nn.functional.cosine_similarity(o, w, dim=0).item()
+    norm_err = (o - w).abs().mean().item() / (w.abs().mean().item() + 1e-9)
+    print(f"P1 cosine {cos:.6f}, normalised error {norm_err:.2e}", flush=True)
+    assert cos >= 0.99 and norm_err <= 0.01
+    assert not torch.allclose(cn.float(), c0.float(), atol=1e-6)
+
+
+def test_p2_bf16_rounded_coefficients(dev):
+    b, nh, deg = 2, 8, 4
+    gen = torch.Generator().manual_seed(12)
+    x = torch.randn(b, 256, D, generator=gen).to(dev)
+    c = torch.randn(b, nh, deg, D // nh, generator=gen).to(dev)
+    m = torch.zeros_like(c)
+    out_f, *_ = K10.apply_cheby_rkv_v10(x, c.clone(), m.clone(), n_heads=nh, seq_threshold=0)
+    out_b, *_ = K10.apply_cheby_rkv_v10(x, c.to(torch.bfloat16).float(), m.clone(), n_heads=nh, seq_threshold=0)
+    rel = (out_f - out_b).abs().max().item() / (out_f.abs().max().item() + 1e-9)
+    print(f"P2 relative error {rel:.2e}", flush=True)
+    assert rel <= 0.015
+
+
+def test_p4_single_chunk_gradients_finite(dev):
+    b, nh, deg = 2, 8, 4
+    gen = torch.Generator().manual_seed(14)
+    xg = torch.randn(b, 256, D, generator=gen).to(dev).requires_grad_(True)
+    cg = torch.randn(b, nh, deg, D // nh, generator=gen).to(dev).requires_grad_(True)
+    out, _, _ = K10.apply_cheby_rkv_v10(xg, cg, torch.zeros(b, nh, deg, D // nh, device=dev), n_heads=nh,
+                                        seq_threshold=0, chunk_size=512)
+    out.sum().backward()
+    torch.cuda.synchronize()
+    assert xg.grad is not None and torch.isfinite(xg.grad).all()
+    assert cg.grad is not None and torch.isfinite(cg.grad).all()
+
+
+def test_p5_latency_within_the_reference_bound(dev):
+    x = torch.randn(2, 1024, 128, generator=torch.Generator().manual_seed(15)).to(dev)
+    c = torch.randn(2, 8, 4, 16, generator=torch.Generator().manual_seed(16)).to(dev)
+    m = torch.zeros_like(c)
+    for _ in range(5):
+        K10.apply_cheby_rkv_v10(x, c.clone(), m.clone(), n_heads=8, seq_threshold=0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        K10.apply_cheby_rkv_v10(x, c.clone(), m.clone(), n_heads=8, seq_threshold=0)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / 20 * 1e3
+    print(f"P5 {ms:.3f} ms per forward (B=2 S=1024 D=128, host included)", flush=True)
+    assert ms <= 3.0
