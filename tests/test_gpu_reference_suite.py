@@ -10,6 +10,7 @@ T15-T17: imports, the layer bus, the full model, the local refiner) are
 outside this path.  From precision_tests.py: P1 (a one-chunk call equals
 the plain series + EMA), P2 (bf16-rounded coefficients move the output by
 <= 1.5%), P4 (one-chunk gradients finite) and P5 (<= 3 ms per forward).
+From gradient_checker.py: its three levels on its own case.
 Where it is cheap the outputs are also compared with the CPU oracle
 (oracle/v10_full.py)."""
 import time
@@ -196,3 +197,60 @@ def test_p5_latency_within_the_reference_bound(dev):
     ms = (time.perf_counter() - t0) / 20 * 1e3
     print(f"P5 {ms:.3f} ms per forward (B=2 S=1024 D=128, host included)", flush=True)
     assert ms <= 3.0
+
+
+def test_gradient_checker_three_levels(dev):
+    """The reference's gradient checker (gradient_checker.py:284-330, 154-228)
+    on its own case, B=1 S=16 D=16 NH=2 deg=4, coefficients N(0,1)*0.05, one
+    upstream gradient, through apply_cheby_rkv_core (S < seq_threshold: the
+    fast path).  L1: the forward matches the reference path (here the
+    float64 oracle, fp32 tolerance); L2: dL/dx and dL/dc from autograd
+    through the drop-in match the reference's analytic gradients (1e-3);
+    L3: the reference's analytic gradient matches central differences with
+    the checker's epsilons (median over them) with cosine > 0.9999 and
+    relative error < 0.005, as it requires (in float64 here)."""
+    from oracle import cheby_ema as O
+    from orthossm_amd.sdpc_kernel import v10_damping
+
+    torch.manual_seed(42)
+    b, s, d, nh, deg = 1, 16, 16, 2, 4
+    hd = d // nh
+    x = torch.randn(b, s, d)
+    coeffs = torch.randn(b, nh, deg, hd) * 0.05
+    grad_out = torch.randn(b, s, d)
+    xg = x.to(dev).requires_grad_(True)
+    cg = coeffs.to(dev).requires_grad_(True)
+    out, *_ = K10.apply_cheby_rkv_core(xg, cg, torch.zeros(b, nh, deg, hd, device=dev), n_heads=nh, ema_momentum=0.9)
+    out.backward(grad_out.to(dev))
+    torch.cuda.synchronize()
+
+    damp = v10_damping(nh).numpy()
+    lam = np.full(nh, 0.9, dtype=np.float32)
+    xd, cd, god = x.double().numpy(), coeffs.double().numpy(), grad_out.double().numpy()
+    fwd = lambda xx, cc: O.forward(xx, cc, damp, lam, nan_policy="zero_u")[0]      # noqa: E731
+    want = fwd(xd, cd)
+    # L1
+    assert np.max(np.abs(out.detach().cpu().numpy() - want)) <= 1e-5 * np.max(np.abs(want)) + 1e-6
+    # L2
+    gx, gc, _ = O.backward(xd, cd, damp, lam, god, nan_policy="zero_u", out_saved=want)
+    for got, w, what in ((xg.grad, gx, "dL/dx"), (cg.grad, gc, "dL/dc")):
+        g = got.cpu().double().numpy()
+        assert np.max(np.abs(g - w)) <= 1e-3 * np.max(np.abs(w)), what
+    # L3 (dL/dx; up to 64 elements, the checker's max_fd_elements)
+    xf = xd.reshape(-1)
+    fd = []
+    for eps in (0.03, 0.05, 0.08, 0.12, 0.2):
+        col = []
+        for i in range(min(xf.size, 64)):
+            h = eps * max(abs(xf[i]), 1.0) * 1e-3
+            xp, xm = xf.copy(), xf.copy()
+            xp[i] += h
+            xm[i] -= h
+            col.append(((fwd(xp.reshape(xd.shape), cd) - fwd(xm.reshape(xd.shape), cd)) * god).sum() / (2 * h))
+        fd.append(col)
+    fd = np.median(np.array(fd), axis=0)
+    an = gx.reshape(-1)[:fd.size]
+    cos = float(an @ fd / (np.linalg.norm(an) * np.linalg.norm(fd)))
+    rel = float(np.linalg.norm(an - fd) / (np.linalg.norm(an) + 1e-8))
+    print(f"L3 cosine {cos:.8f}, relative error {rel:.2e}", flush=True)
+    assert cos > 0.9999 and rel < 0.005
