@@ -6,8 +6,9 @@ and bf16 input and output, an initial EMA state, strided (non-contiguous)
 x, both NaN policies, the output clamp on and off, and a few special values
 (NaN, +-Inf, huge, subnormal) planted in x; for the full path also chunk
 sizes, the LUT and Clenshaw series, the complexity gate, dynamic lambda and
-the Lion hyperparameters.  Each case is drawn from its own seed, so a
-failure names a reproducible configuration."""
+the Lion hyperparameters; the full path's gradients; and the engine's
+call sites.  Each case is drawn from its own seed, so a failure names a
+reproducible configuration."""
 import numpy as np
 import pytest
 import torch
@@ -224,3 +225,84 @@ def test_random_full_path_gradients(dev, seed):
         assert_close_grad(cd.grad.cpu(), wc, what="grad_coeffs")
     else:
         assert cd.grad is None
+
+
+def _engine_host_steps_f64(m, x, tokens_before, state):
+    """The engine's steps before its call into the op, in float64 on the CPU
+    from the module's weights (sdpc_engine.py:163-209): RMSNorm (eps = fp32
+    machine epsilon), token mean, coefficients coeff_init_proj(mean) *
+    0.1/(k+1) (or the given state), gate sigmoid(MLP(mean)), mu from the
+    token count after this call.  Returns (x_normed, coeffs, momentum, gate,
+    mu)."""
+    import math
+
+    import torch.nn.functional as F
+    W = {k: v.detach().cpu().double() for k, v in m.state_dict().items()}
+    xd = x.detach().cpu().double()
+    b, s, d = xd.shape
+    h, k_terms, hd = m.n_cheby_heads, m.max_degree, m.head_dim
+    xn = xd * torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + torch.finfo(torch.float32).eps) * W["input_norm.weight"]
+    xm = xn.mean(dim=1)
+
+    def mlp(prefix, v):
+        hid = F.silu(v @ W[f"{prefix}.0.weight"].T + W[f"{prefix}.0.bias"])
+        return hid @ W[f"{prefix}.2.weight"].T + W[f"{prefix}.2.bias"]
+
+    if state is None:
+        kk = torch.arange(k_terms, dtype=torch.float64)
+        c = mlp("coeff_init_proj", xm).view(b, h, k_terms, hd) * (0.1 / (kk + 1.0)).view(1, 1, k_terms, 1)
+        mom = torch.zeros_like(c)
+    else:
+        c, mom = state[0].cpu().double(), state[1].cpu().double()
+    gate = torch.sigmoid(mlp("complexity_gate.net", xm)).reshape(b)
+    p = min((tokens_before + s) / 1e8, 1.0)
+    mu = 0.7 + 0.5 * (float(W["ema_base"]) - 0.7) * (1.0 + math.cos(math.pi * p))
+    return xn, c, mom, gate, mu
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_engine_routes(dev, seed):
+    """The engine's call sites with random widths, heads, degrees, chunk
+    sizes, lengths (all three routes), token counts and incoming state,
+    against the oracle fed with the engine's host steps."""
+    from oracle import cheby_ema as O
+    from orthossm_amd import engine as E
+
+    r = np.random.default_rng(6000 + seed)
+    d = int(r.choice((64, 128, 256)))
+    h = int(r.choice([v for v in (2, 4, 8) if d % v == 0]))
+    k_terms = int(r.choice((4, 8)))
+    chunk = int(r.choice((128, 256)))
+    s = int(r.integers(16, 1500))
+    b = int(r.integers(1, 4))
+    tokens_before = int(r.integers(0, 100_000_000))
+    torch.manual_seed(seed)
+    m = E.ChebyContextPath(d, n_cheby_heads=h, max_degree=k_terms, chunk_size=chunk).to(dev)
+    torch.nn.init.normal_(m.coeff_init_proj[-1].weight, std=0.5)
+    with torch.no_grad():
+        m.input_norm.weight.uniform_(0.5, 1.5, generator=torch.Generator(device=dev).manual_seed(seed))
+        m.total_tokens_seen.fill_(tokens_before)
+    state = None
+    if r.random() < 0.4:
+        g = torch.Generator().manual_seed(seed + 1)
+        state = ((torch.randn(b, h, k_terms, d // h, generator=g) * 0.1).to(dev),
+                 (torch.randn(b, h, k_terms, d // h, generator=g) * 0.01).to(dev))
+    x = torch.randn(b, s, d, generator=torch.Generator().manual_seed(seed + 2)) * 1.5
+    print(f"d={d} h={h} K={k_terms} chunk={chunk} B={b} S={s} tokens_before={tokens_before} "
+          f"state={state is not None}", flush=True)
+    with torch.no_grad():
+        res = m(x.to(dev), state)
+    torch.cuda.synchronize()
+    assert res.route == E.route(s)
+    xn, c, mom, gate, mu = _engine_host_steps_f64(m, x, tokens_before, state)
+    assert abs(float(res.ema_momentum) - mu) <= 1e-7
+    assert_close_fp32(res.x_normed.cpu(), xn.numpy(), what="x_normed")
+    if res.route == "fast":
+        damping = 0.98 - 0.06 * np.arange(h) / h
+        want, _ = O.forward(xn.numpy(), c.numpy(), damping, np.full(h, mu), nan_policy="zero_u")
+        assert_close_fp32(res.out.cpu(), want)
+        assert_close_fp32(res.state[0].cpu(), c.numpy(), what="coeffs")
+    else:
+        want = V.v10_full(xn.float().numpy(), c.numpy(), mom.numpy(), n_heads=h, base_lr=0.005, ema_momentum=mu,
+                          gate_global=gate.numpy(), dynamic_lambda=gate.numpy(), use_lut=True, chunk_size=chunk)
+        compare_v10(res.out, res.state[0], res.state[1], want)
