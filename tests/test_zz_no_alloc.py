@@ -2,8 +2,10 @@
 library's static device array, no allocation) through the C ABI: the same
 bits as osm_cheby_ema_fwd with a caller workspace on two calls in a row, the
 second with a smaller input, static and dynamic lambda, with the EMA carry;
-its fault word (osm_workspace_status with a NULL workspace) stays zero; a
-shape whose workspace exceeds the static array is refused before any launch."""
+a seeded sequence of twelve calls of changing layouts gives the same bits
+as well; its fault word (osm_workspace_status with a NULL workspace) stays
+zero; a shape whose workspace exceeds the static array is refused before
+any launch."""
 import ctypes
 
 import pytest
@@ -103,3 +105,28 @@ def test_static_scratch_refuses_shapes_beyond_its_size(dev):
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())          # nothing was launched
     del keep
+
+
+def test_static_scratch_random_sequence_of_layouts(dev):
+    """A seeded sequence of calls whose layouts change from call to call
+    (batch, length, heads, head size, terms, static or dynamic lambda, an
+    initial state): every call gives the bits of the workspace entry point."""
+    import numpy as np
+
+    lib = nat.load()
+    r = np.random.default_rng(73)
+    for i in range(12):
+        H = int(r.choice((1, 2, 4, 8)))
+        hd = int(r.choice((8, 16, 32, 64)))
+        B = int(r.integers(1, 4))
+        S = int(r.integers(1, 6000))
+        K = int(r.integers(1, 9))
+        dyn = bool(r.random() < 0.4)
+        d = to_dev(inputs(B, S, H, hd, K, seed=100 + i, dynamic=dyn), dev)
+        init = None
+        if r.random() < 0.5:
+            init = (torch.rand(B, H * hd, generator=torch.Generator().manual_seed(i)) - 0.5).to(dev)
+        (out_s, fin_s), (out_w, fin_w) = run_both(lib, dev, d, init)
+        assert torch.equal(out_s, out_w), (i, B, S, H, hd, K, dyn)
+        assert torch.equal(fin_s, fin_w), (i, B, S, H, hd, K, dyn)
+    assert static_status(lib, dev)[0] == 0
