@@ -43,7 +43,20 @@ def common_flags() -> list[str]:
 
 
 def compile_command(out: str) -> list[str]:
+    """One-step build of the whole library (kept for reference and tooling;
+    build() compiles the sources in parallel and links them)."""
     return [hipcc_path(), *common_flags(), "-shared", "-o", out, *sources()]
+
+
+OBJ_DIR = os.path.join(PKG_DIR, "_build")
+
+
+def object_command(src: str, obj: str) -> list[str]:
+    return [hipcc_path(), *common_flags(), "-c", "-o", obj, src]
+
+
+def link_command(objs: list[str], out: str) -> list[str]:
+    return [hipcc_path(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out, *objs]
 
 
 def device_asm_command(src: str, out: str) -> list[str]:
@@ -54,16 +67,38 @@ def device_asm_command(src: str, out: str) -> list[str]:
 def build(verbose: bool = False) -> str:
     """Compiles the library (always, even if one exists) and returns its path."""
     os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + f".tmp{os.getpid()}"
-    cmd = compile_command(tmp)
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        if os.path.exists(tmp):
-            os.remove(tmp)
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-8000:]}")
-    os.replace(tmp, LIB_PATH)
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    tag = os.getpid()
+    objs, procs = [], []
+    # One hipcc per source, all at once (each kernel file is its own
+    # translation unit), then one link.
+    for src in sources():
+        obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + f".{tag}.o")
+        cmd = object_command(src, obj)
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        objs.append(obj)
+        procs.append(subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True))
+    errors = []
+    for src, pr in zip(sources(), procs):
+        _, err = pr.communicate()
+        if pr.returncode != 0:
+            errors.append(f"{os.path.basename(src)}: hipcc failed ({pr.returncode}):\n{err[-8000:]}")
+    tmp = LIB_PATH + f".tmp{tag}"
+    try:
+        if errors:
+            raise RuntimeError("\n".join(errors))
+        cmd = link_command(objs, tmp)
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"link failed ({res.returncode}):\n{res.stderr[-8000:]}")
+        os.replace(tmp, LIB_PATH)
+    finally:
+        for f in objs + [tmp]:
+            if os.path.exists(f):
+                os.remove(f)
     build_c_smoke(verbose)
     return LIB_PATH
 
