@@ -52,7 +52,9 @@
  *     calls: a launch counter and tagged look-back words.  The library clears
  *     it on the stream the first time it sees a workspace pointer (unless
  *     osm_workspace_init zeroed it) and whenever the layout changes (shape,
- *     K class, static/dynamic lambda, entry point).  A workspace freed and a new
+ *     K class, static/dynamic lambda, entry point); such a clear keeps the
+ *     header's first 64 bytes (launch counter, fault word) and zeroes its
+ *     completion counters and the look-back words.  A workspace freed and a new
  *     one allocated at the same address must be passed through
  *     osm_workspace_init.  Two calls that overlap in time must not share one
  *     workspace; if they do, every wave still exits (bounded waits) and the
@@ -104,6 +106,16 @@ typedef enum osm_status {
                                       before it combines the words it read, to
                                       perturb the order in which tiles finish;
                                       results are unchanged, bit for bit */
+#define OSM_FLAG_POLL_LIMIT_ZERO 0x10 /* test aid, no counterpart in the reference:
+                                      a look-back wait whose word is not yet
+                                      published when first read gives up at
+                                      once instead of polling, as a wait that
+                                      passes its poll limit does: the fault
+                                      word is set and the outputs that depend
+                                      on the missing value are NaN (out,
+                                      ema_final, the TTT gradient, the
+                                      backward's gradients); every kernel
+                                      still exits normally */
 
 /* TTT target y */
 typedef enum osm_ttt_target { OSM_TARGET_X = 0, OSM_TARGET_SOFTSIGN = 1 } osm_ttt_target;
@@ -241,8 +253,10 @@ const char* osm_last_error(void);
 /* Workspace bytes needed by osm_cheby_ema_fwd (op = OSM_OP_FWD),
  * osm_cheby_ema_ttt (OSM_OP_TTT) or osm_cheby_ema_bwd (OSM_OP_BWD).  Reads
  * only the shape fields, dtypes, K, whether g is NULL and (forward) the x/out
- * strides and pointer alignment that choose its geometry; returns 0 if those
- * are invalid. */
+ * strides and pointer alignment that choose its geometry; with x or out NULL
+ * the forward is sized for its one-lane geometry, which needs the most (so
+ * the size serves any later x/out of that shape).  Returns 0 if those are
+ * invalid. */
 size_t osm_workspace_bytes(const osm_cheby_args* args, int op);
 
 /* Zero-fill `bytes` of workspace on `stream` with a fill kernel. */

@@ -22,6 +22,7 @@ FLAG_NO_CLAMP = 0x1
 FLAG_NAN_ZERO_U = 0x2
 FLAG_FULL_JACOBIAN = 0x4
 FLAG_TIMING_JITTER = 0x8   # test aid: pseudo-random delays before look-back publishes
+FLAG_POLL_LIMIT_ZERO = 0x10   # test aid: a look-back wait gives up at its first unpublished read
 TARGET_X = 0
 TARGET_SOFTSIGN = 1
 OP_FWD = 0

@@ -63,7 +63,7 @@ int check_args(const osm_cheby_args* a, Geometry* geo, int op, bool shapes_only 
   if (!a) return fail(OSM_E_ARG, "args is NULL");
   if (a->abi_version != OSM_ABI_VERSION)
     return fail(OSM_E_ARG, "abi_version %d does not match library ABI %d", a->abi_version, OSM_ABI_VERSION);
-  const int known = OSM_FLAG_NO_CLAMP | OSM_FLAG_NAN_ZERO_U | OSM_FLAG_TIMING_JITTER |
+  const int known = OSM_FLAG_NO_CLAMP | OSM_FLAG_NAN_ZERO_U | OSM_FLAG_TIMING_JITTER | OSM_FLAG_POLL_LIMIT_ZERO |
                     (op == OSM_OP_BWD ? OSM_FLAG_FULL_JACOBIAN : 0);
   if (a->flags & ~known) return fail(OSM_E_ARG, "unknown flag bits 0x%x", a->flags);
   if (a->B < 0 || a->S < 0) return fail(OSM_E_SHAPE, "B=%lld and S=%lld must be >= 0", (long long)a->B, (long long)a->S);
@@ -83,8 +83,11 @@ int check_args(const osm_cheby_args* a, Geometry* geo, int op, bool shapes_only 
   geo->empty = a->B == 0 || a->S == 0;
   const int xs = a->x_dtype == OSM_F32 ? 4 : 2;
   const int os = a->out_dtype == OSM_F32 ? 4 : 2;
-  const bool rows4 = a->hd % 4 == 0 && aligned4(a->x, xs) && a->x_stride_b % 4 == 0 && a->x_stride_s % 4 == 0 &&
-                     aligned4(a->out, os) && a->out_stride_b % 4 == 0 && a->out_stride_s % 4 == 0;
+  // A shapes-only query with x or out NULL does not know their alignment:
+  // it is sized for the one-lane geometry, the largest workspace.
+  const bool rows4 = a->hd % 4 == 0 && a->x && aligned4(a->x, xs) && a->x_stride_b % 4 == 0 &&
+                     a->x_stride_s % 4 == 0 && a->out && aligned4(a->out, os) && a->out_stride_b % 4 == 0 &&
+                     a->out_stride_s % 4 == 0;
   const bool generic = op == OSM_OP_FWD && (!rows4 || a->K > osm::kMonoMaxK);
   if (geo->empty) return OSM_OK;
   // The backward reads out only for the clamp mask.
@@ -177,6 +180,7 @@ osm::FwdParams make_params(const osm_cheby_args* a, const Geometry& geo, void* w
   p.clamp_out = (a->flags & OSM_FLAG_NO_CLAMP) ? 0 : 1;
   p.nan_zero_u = (a->flags & OSM_FLAG_NAN_ZERO_U) ? 1 : 0;
   p.jitter = (a->flags & OSM_FLAG_TIMING_JITTER) ? 1 : 0;
+  p.poll_limit = (a->flags & OSM_FLAG_POLL_LIMIT_ZERO) ? 0u : osm::kSpinLimit;
   return p;
 }
 
@@ -233,9 +237,11 @@ int prepare_workspace(void* ws, size_t need, const Geometry& geo, int op, hipStr
     g_ws_layout[(uintptr_t)ws] = now;
   }
   if (clear) {
-    // A known workspace keeps its header (epoch, fault word): only the
-    // look-back words are cleared.
-    const size_t skip = fresh ? 0 : osm::kHeaderBytes;
+    // A known workspace keeps the start of its header (launch epoch, fault
+    // word); the completion counters after it and the look-back words are
+    // cleared, which also repairs counters that overlapping calls (misuse)
+    // left behind.
+    const size_t skip = fresh ? 0 : osm::kHeaderKeepBytes;
     const hipError_t e = osm::launch_fill_zero(static_cast<char*>(ws) + skip, need - skip, stream);
     if (e != hipSuccess) {
       std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -376,7 +382,7 @@ int osm_cheby_ema_fwd_static(const osm_cheby_args* args, void* stream) {
     std::lock_guard<std::mutex> lk(g_static_mu);
     StaticScratch& sc = g_static[dev];
     clear = !sc.used || !(sc.layout == now);
-    skip = sc.used ? osm::kHeaderBytes : 0;   // a used scratch keeps its header (launch counter)
+    skip = sc.used ? osm::kHeaderKeepBytes : 0;   // a used scratch keeps its launch counter and fault word
     sc.used = true;
     sc.layout = now;
   }
@@ -559,6 +565,8 @@ int osm_cheby_ema_bwd(const osm_cheby_args* args, const osm_cheby_bwd_args* bwd,
   if (bwd->z_saved) {
     if (geo.dyn || args->out_dtype != OSM_F32)
       return fail(OSM_E_ARG, "z_saved needs a static lambda and an fp32 out");
+    if (args->K > osm::kMonoMaxK)
+      return fail(OSM_E_ARG, "z_saved needs K <= %d (K=%lld)", osm::kMonoMaxK, (long long)args->K);
     if ((uintptr_t)bwd->z_saved % 2 || bwd->z_stride_b < 0 || bwd->z_stride_s < 0 ||
         (tile_rows * bwd->z_stride_s + D) * 2 >= (int64_t(1) << 31))
       return fail(OSM_E_LAYOUT, "z_saved must be bf16-aligned with non-negative strides fitting 31-bit offsets");

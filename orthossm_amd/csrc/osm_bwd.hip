@@ -97,12 +97,14 @@ __device__ __forceinline__ void accumulate_basis(float (&Gk)[KP], float e, float
 // the fast variant assumes none of them occurs in the run.  ZS: 1 - z^2 comes
 // from the saved z (zv) instead of the recomputed series.  full_jac: dL/dx
 // uses 1/(1+|x|)^2 everywhere (NaN for a NaN x) instead of 0 below 1e-7.
+// cheb (slow variant only): c and dm are in the Chebyshev form of a tile
+// whose monomial coefficients exceed kMonoBound.
 template <class G, bool DYN, bool SLOW, bool ZS, typename XT, int KP>
 __device__ __forceinline__ void bwd_pass2(float& v, float (&Gk)[KP], const float (&xv)[G::R], const float (&gv)[G::R],
                                           const float (&zv)[ZS ? G::R : 1], const float (&lamv)[G::R], float lam_h,
                                           const float (&c)[KP], const float (&dm)[KP > 1 ? KP - 1 : 1],
                                           const RowStream& gx, int n_valid, unsigned mbits, bool nan_zero_u,
-                                          bool full_jac) {
+                                          bool full_jac, bool cheb) {
   constexpr int R = G::R;
   uint32_t so = (uint32_t)(R - 1) * gx.s;
   asm volatile("" : "+s"(so));
@@ -126,17 +128,24 @@ __device__ __forceinline__ void bwd_pass2(float& v, float (&Gk)[KP], const float
     if constexpr (ZS) {
       hq = 0.25f * __builtin_fmaf(-zv[r], zv[r], 1.0f);
     } else {
-      const float rr = tanh_r(series<KP>(u, c));
+      float y;
+      if (SLOW && cheb)
+        y = series_as<KP, true>(u, c);
+      else
+        y = series_as<KP, false>(u, c);
+      const float rr = tanh_r(y);
       hq = __builtin_fmaf(-rr, rr, rr);
     }
     float e = av * hq;
     if constexpr (DYN) e *= 1.0f - lam;
     if constexpr (SLOW) e = live ? e : 0.0f;
     float dy = 0.0f;
-    if constexpr (KP > kMonoMaxK)
-      dy = clenshaw_u<KP - 1>(u, dm);
-    else if constexpr (KP > 1)
-      dy = horner<KP - 1>(u, dm);
+    if constexpr (KP > 1) {
+      if (SLOW && cheb)
+        dy = dseries_as<KP - 1, true>(u, dm);
+      else
+        dy = dseries_as<KP - 1, false>(u, dm);
+    }
     float gxv[1] = {e * dy * ir * ir};
     if (!full_jac) gxv[0] = __builtin_fabsf(x) >= kSoftsignGradMin ? gxv[0] : 0.0f;
     BufVec<XT, 1>::store(gx.r, gx.v, so, gxv);
@@ -217,7 +226,8 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
     }
   }
   __builtin_amdgcn_s_setprio(0);
-  mono_store<KP, G>(ml, q, mono);   // read after the chain's barriers
+  __shared__ unsigned mono_big[KP * G::NSUB];
+  mono_store<KP, G>(ml, q, mono, mono_big);   // read after the chain's barriers
 
   // Pass 1: the run's map v[t0] = A v[t_end + 1] + B, last token first.
   // Tokens of this run that are < S (wave-uniform: one run per wave).
@@ -294,12 +304,20 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
     LookBack<G, true> lbk;
     look_back_issue<G, true>(lbk, q, ti, ls);
     jitter(p.jitter, tags.epoch, 1);
-    look_back_finish<G, true>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, 0.0f, p.hdr);
+    look_back_finish<G, true>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, 0.0f, p.hdr, p.poll_limit);
   }
   float v = __builtin_fmaf(pA, L.carry[q.lt], pB[0]);
 
   // Pass 2.
   float c[1][KP];
+  // Monomial form unless a coefficient of the tile exceeds kMonoBound; a
+  // tile in the Chebyshev form (rare with up to kMonoMaxK coefficients)
+  // rewrites the table and takes the slow pass 2, which evaluates either.
+  const bool cheb = tile_cheb<KP, G>(mono_big);
+  if (KP <= kMonoMaxK && cheb) {
+    mono_store_cheb<KP, G>(p, q, ti, a, mono);
+    __syncthreads();
+  }
   mono_read<G, KP>(mono, q, c);
   float dm[KP > 1 ? KP - 1 : 1];
   {
@@ -315,12 +333,13 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
 #pragma unroll
   for (int r = 0; r < R; ++r) bad |= xv[r] != xv[r];
   const bool full_jac = bp.full_jac != 0;
-  if (slow1 || bad)
+  const bool cheb2 = KP <= kMonoMaxK && cheb;   // (above kMonoMaxK both variants use Clenshaw)
+  if (slow1 || bad || cheb2)
     bwd_pass2<G, DYN, true, ZS, XT, KP>(v, Gk, xv, gv, zv, lamv, lam_h, c[0], dm, gx, n_valid, mbits,
-                                        p.nan_zero_u != 0, full_jac);
+                                        p.nan_zero_u != 0, full_jac, cheb2);
   else
     bwd_pass2<G, DYN, false, ZS, XT, KP>(v, Gk, xv, gv, zv, lamv, lam_h, c[0], dm, gx, n_valid, 0u, false,
-                                         full_jac);
+                                         full_jac, false);
 
   // dL/d ema_init = v[0], held by the first run of tile 0.
   if (tm.tile == 0 && q.tg == 0 && bp.grad_init) {

@@ -220,13 +220,14 @@ __device__ __forceinline__ void look_back_issue(LookBack<G, DYN>& st, const Thre
 }
 
 // `a_look` is the full-tile decay static_tile_A of look_lane's static lambda
-// (unused when DYN); `init_carry`
-// the initial state of carry_lane (waves < NSUB).
+// (unused when DYN); `init_carry` the initial state of carry_lane (waves <
+// NSUB); `limit` the poll limit of await_word.  A wait that gives up yields
+// NaN, so the carry (and a checkpoint published from it) is NaN.
 template <class G, bool DYN>
 __device__ __forceinline__ void look_back_finish(LookBack<G, DYN>& st, ChainLds<G>& L, const ThreadPos& q,
                                                  const TileInfo& ti, const Tags& tg, float aggA, float aggB,
                                                  const LaneSlots& ls, float init_carry, float a_look,
-                                                 unsigned* hdr_words) {
+                                                 unsigned* hdr_words, unsigned limit) {
   if (ti.tile > 0) {
     const int ll = look_lane<G>(q);
     float mA = 1.0f, mB = 0.0f;
@@ -236,9 +237,9 @@ __device__ __forceinline__ void look_back_finish(LookBack<G, DYN>& st, ChainLds<
       for (int i = 0; i < G::WPT; ++i) {
         if (st.beg + i < st.end) {
           const unsigned long long* s = ls.at(st.beg + i, ll);
-          const float Bp = await_word(s, st.vB[i], tg.agg, hdr_words);
+          const float Bp = await_word(s, st.vB[i], tg.agg, hdr_words, limit);
           float Ap = Afull;
-          if constexpr (DYN) Ap = await_word(s + 1, st.vA[i], tg.agg, hdr_words);
+          if constexpr (DYN) Ap = await_word(s + 1, st.vA[i], tg.agg, hdr_words, limit);
           mB = __builtin_fmaf(Ap, mB, Bp);
           mA *= Ap;
         }
@@ -248,7 +249,7 @@ __device__ __forceinline__ void look_back_finish(LookBack<G, DYN>& st, ChainLds<
     L.mB[q.wave][q.wl] = mB;
     float ck = init_carry;
     if (q.wave < G::NSUB && st.g0 > 0)
-      ck = await_word(ls.at(st.g0 - 1, carry_lane<G>(q)), st.vck, tg.pre, hdr_words);
+      ck = await_word(ls.at(st.g0 - 1, carry_lane<G>(q)), st.vck, tg.pre, hdr_words, limit);
     __syncthreads();
     if (q.wave < G::NSUB) {
       const int w0 = q.wave * G::WPS;   // the waves that read this sub-block

@@ -45,12 +45,8 @@ struct WsHeader {
   } cls[8];                // byte offsets 128 + 128 c
 };
 static_assert(sizeof(WsHeader) <= kHeaderBytes, "header fits");
-
-// Upper bound on polls of one look-back word (each poll is a device-scope
-// load plus a short sleep: about a second in total).  It only guarantees
-// that every wave exits if the dispatch-order assumption of the look-back
-// ever failed or two calls overlapped on one workspace.
-constexpr unsigned kSpinLimit = 1u << 20;
+static_assert(offsetof(WsHeader, fault) < kHeaderKeepBytes && offsetof(WsHeader, done_all) == kHeaderKeepBytes,
+              "a layout change keeps the epoch and the fault word and clears the counters");
 
 // A look-back word is one 64-bit value: high 32 bits = (epoch << 2) | kind,
 // low 32 bits = an fp32 payload.  Because tag and payload travel in one
@@ -81,21 +77,24 @@ __device__ __forceinline__ void raise_fault(unsigned* hdr_words, unsigned fault_
 // Spin until `slot` carries `tag`, starting from an already-loaded value.
 // The producer of every awaited word was dispatched earlier and publishes
 // without waiting on anything later (osm_chain.h), so the loop ends;
-// kSpinLimit bounds it anyway (fault word set to this launch's fault tag,
-// payload 0).
+// `limit` polls (kSpinLimit, or 0 under OSM_FLAG_POLL_LIMIT_ZERO) bound it
+// anyway.  A wait that gives up sets the fault word to this launch's fault
+// tag and returns a quiet NaN: every carry composed from it is NaN, so the
+// outputs that depend on the missing value are NaN (the kernels store a NaN
+// state unclamped), not plausible numbers.
 __device__ __forceinline__ float await_word(const unsigned long long* slot, unsigned long long w, unsigned tag,
-                                            unsigned* hdr_words) {
+                                            unsigned* hdr_words, unsigned limit) {
   unsigned polls = 0;
   while ((unsigned)(w >> 32) != tag) {
     ++polls;
     // Give up when over the limit or when another wave of this launch
     // already gave up (a fault left by an earlier launch is ignored).
     const unsigned ftag = fault_tag_of(tag);
-    if (polls > kSpinLimit ||
+    if (polls > limit ||
         ((polls & 1023u) == 0 &&
          __hip_atomic_load(hdr_words + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ftag)) {
       raise_fault(hdr_words, ftag);
-      return 0.0f;
+      return __builtin_nanf("");
     }
     __builtin_amdgcn_s_sleep(1);
     w = peek(slot);
@@ -376,6 +375,17 @@ __device__ __forceinline__ float series(float u, const float (&c)[KP]) {
     return horner<KP>(u, c);
 }
 
+// The series in the form a tile chose: CHEB (or more than kMonoMaxK
+// coefficients) = Chebyshev coefficients by Clenshaw, else monomial
+// coefficients by Horner.
+template <int KP, bool CHEB>
+__device__ __forceinline__ float series_as(float u, const float (&c)[KP]) {
+  if constexpr (CHEB || KP > kMonoMaxK)
+    return clenshaw<KP>(u, c);
+  else
+    return horner<KP>(u, c);
+}
+
 // Clenshaw evaluation of sum_{m<N} d[m] U_m(u) in the second-kind basis
 // (U_0 = 1, U_1 = 2u, U_m = 2u U_{m-1} - U_{m-2}):
 //   b_m = d_m + 2u b_{m+1} - b_{m+2},  sum = b_0.
@@ -392,6 +402,17 @@ __device__ __forceinline__ float clenshaw_u(float u, const float (&d)[N]) {
     b1 = b0;
   }
   return b1;
+}
+
+// The derivative of series_as from dm[m] = (m+1) c[m+1] (times a scale):
+// sum dm[m] U_m(u) by Clenshaw in the Chebyshev form (T_k' = k U_{k-1}),
+// sum dm[m] u^m by Horner in the monomial form.
+template <int N, bool CHEB>
+__device__ __forceinline__ float dseries_as(float u, const float (&dm)[N]) {
+  if constexpr (CHEB || N + 1 > kMonoMaxK)
+    return clenshaw_u<N>(u, dm);
+  else
+    return horner<N>(u, dm);
 }
 
 // x^N by repeated squaring in float64, rounded once to fp32 (within about

@@ -16,6 +16,8 @@
 //   5. pass 2: replay s = lam*s + w from the carry, store out.
 // All tensor traffic uses buffer descriptors (osm_device.h): no per-element
 // address arithmetic and no bounds branches.
+#include <type_traits>
+
 #include "osm_tile.h"
 
 namespace osm {
@@ -26,21 +28,24 @@ namespace {
 // sdpc_kernel.py:1725.
 template <int KP>
 __device__ __forceinline__ float ema_input_exact(float x, const float (&a)[KP], float one_m, float neg2_one_m,
-                                                 bool nan_zero_u) {
+                                                 bool nan_zero_u, bool cheb) {
   const bool ok = x == x;
-  const float r = tanh_r(series<KP>(ok ? softsign(x) : 0.0f, a));
+  const float u = ok ? softsign(x) : 0.0f;
+  const float r = tanh_r(cheb ? series_as<KP, true>(u, a) : series_as<KP, false>(u, a));
   const float w = __builtin_fmaf(neg2_one_m, r, one_m);
   return (ok || nan_zero_u) ? w : 0.0f;
 }
 
 // Rare path: a run whose aggregate is NaN saw a NaN or infinite input (or
 // non-finite coefficients).  Reload its x and recompute with the exact
-// special-value handling.
+// special-value handling, in the series form of the tile (cheb: Clenshaw).
 template <class G, bool DYN, typename XT, int KP>
 __device__ __forceinline__ void pass1_exact(float (&w)[G::R][G::LPT], const TileAddr& a, const float (&c)[G::LPT][KP],
-                                            const float (&lamv)[G::R], float (&Bv)[G::LPT], bool nan_zero_u) {
+                                            const float (&lamv)[G::R], float (&Bv)[G::LPT], bool nan_zero_u,
+                                            bool cheb) {
 #pragma unroll
   for (int i = 0; i < G::LPT; ++i) Bv[i] = 0.0f;
+#pragma unroll
   for (int r = 0; r < G::R; ++r) {
     float xv[G::LPT];
     BufVec<XT, G::LPT>::load(a.x, a.vx, (uint32_t)r * a.sx, xv);
@@ -49,7 +54,7 @@ __device__ __forceinline__ void pass1_exact(float (&w)[G::R][G::LPT], const Tile
     const float n2 = -2.0f * one_m;
 #pragma unroll
     for (int i = 0; i < G::LPT; ++i) {
-      w[r][i] = ema_input_exact<KP>(xv[i], c[i], one_m, n2, nan_zero_u);
+      w[r][i] = ema_input_exact<KP>(xv[i], c[i], one_m, n2, nan_zero_u, cheb);
       Bv[i] = __builtin_fmaf(lam, Bv[i], w[r][i]);
     }
   }
@@ -57,8 +62,10 @@ __device__ __forceinline__ void pass1_exact(float (&w)[G::R][G::LPT], const Tile
 
 // Pass 2 over a thread's run: s = lam*s + w from the carried state, out =
 // clamp(s, lo, hi).  FINAL: also stores the state at run index r_fin to fin
-// (when fin is non-NULL).
-template <class G, typename OT, bool FINAL>
+// (when fin is non-NULL).  NANP: a NaN state is stored as NaN (the clamp,
+// v_med3_f32, would return a bound); taken when the carried state is NaN,
+// which a look-back wait that gave up leaves (or a NaN ema_init).
+template <class G, typename OT, bool FINAL, bool NANP>
 __device__ __forceinline__ void pass2(float (&s)[G::LPT], const float (&w)[G::R][G::LPT], const float (&lamv)[G::R],
                                       const TileAddr& a, float lo, float hi, int r_fin, float* fin) {
   uint32_t so = 0;
@@ -69,6 +76,7 @@ __device__ __forceinline__ void pass2(float (&s)[G::LPT], const float (&w)[G::R]
     for (int i = 0; i < G::LPT; ++i) {
       s[i] = __builtin_fmaf(lamv[r], s[i], w[r][i]);
       o[i] = __builtin_amdgcn_fmed3f(s[i], lo, hi);
+      if constexpr (NANP) o[i] = s[i] == s[i] ? o[i] : s[i];
     }
     if constexpr (FINAL) {
       if (r == r_fin && fin) {
@@ -131,8 +139,16 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   }
 
   __builtin_amdgcn_s_setprio(0);
-  mono_store<KP, G>(ml, q, mono);
+  __shared__ unsigned mono_big[KP * G::NSUB];
+  mono_store<KP, G>(ml, q, mono, mono_big);
   __syncthreads();
+  // Monomial form unless a coefficient of the tile exceeds kMonoBound (rare:
+  // the Chebyshev coefficients replace the table, one more barrier).
+  const bool cheb = tile_cheb<KP, G>(mono_big);
+  if (KP <= kMonoMaxK && cheb) {
+    mono_store_cheb<KP, G>(p, q, ti, a, mono);
+    __syncthreads();
+  }
   float c[LPT][KP];
   mono_read<G, KP>(mono, q, c);
 
@@ -199,7 +215,12 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   bool bad = false;
 #pragma unroll
   for (int i = 0; i < LPT; ++i) bad |= Bv[i] != Bv[i];
-  if (bad) pass1_exact<G, DYN, XT, KP>(w, a, c, lamv, Bv, p.nan_zero_u != 0);
+  // A tile in the Chebyshev form (always above kMonoMaxK coefficients, else
+  // rare) redoes the run in the rare path with Clenshaw: with up to
+  // kMonoMaxK coefficients the loop above, which then ran Horner on the
+  // Chebyshev coefficients, stays the one straight-line pass of the common
+  // case.
+  if (bad || (KP <= kMonoMaxK && cheb)) pass1_exact<G, DYN, XT, KP>(w, a, c, lamv, Bv, p.nan_zero_u != 0, cheb);
   const unsigned fin_prev = finish_issue(p.hdr, tags.epoch);
 
   const LaneSlots ls = lane_slots<G, DYN>(p.slots, ti, p.n_tiles);
@@ -217,7 +238,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     LookBack<G, DYN> lbk;
     look_back_issue<G, DYN>(lbk, q, ti, ls);
     jitter(p.jitter, tags.epoch, 1);
-    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, a_look, p.hdr);
+    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, a_look, p.hdr, p.poll_limit);
   }
   finish_complete(p.hdr, tags.epoch, fin_prev);
 
@@ -227,8 +248,14 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   for (int i = 0; i < LPT; ++i) s[i] = __builtin_fmaf(pA, L.carry[q.lt * LPT + i], pB[i]);
   const float lo = p.clamp_out ? -1.0f : -__builtin_inff();
   const float hi = p.clamp_out ? 1.0f : __builtin_inff();
+  bool nan_s = false;
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) nan_s |= s[i] != s[i];
   if (!ti.is_last) {
-    pass2<G, OT, false>(s, w, lamv, a, lo, hi, 0, nullptr);
+    if (!nan_s)
+      pass2<G, OT, false, false>(s, w, lamv, a, lo, hi, 0, nullptr);
+    else
+      pass2<G, OT, false, true>(s, w, lamv, a, lo, hi, 0, nullptr);
   } else {
     // The last tile also yields ema_final: the unclamped state at token S-1,
     // from the one run that holds it.
@@ -236,7 +263,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     float* fin = (p.ema_final && a.vo != kOffOOB && r_last >= 0 && r_last < R)
                      ? p.ema_final + (int64_t)ti.b * p.D + ti.lbd * G::LANES + q.lt * LPT
                      : nullptr;
-    pass2<G, OT, true>(s, w, lamv, a, lo, hi, r_last, fin);
+    pass2<G, OT, true, true>(s, w, lamv, a, lo, hi, r_last, fin);
   }
 }
 

@@ -107,10 +107,21 @@ using BwdTile = TileGeo<1, 8, 24, 64, 2>;   // 192 tokens
 using BwdTileCheb = TileGeo<1, 8, 12, 64, 2>;   // 96 tokens
 int bwd_tile_tokens(bool dyn, int kpad);
 
+// Upper bound on polls of one look-back word (each poll is a device-scope
+// load plus a short sleep: about a second in total).  It only guarantees
+// that every wave exits if the dispatch-order assumption of the look-back
+// ever failed or two calls overlapped on one workspace.  A launch with
+// OSM_FLAG_POLL_LIMIT_ZERO (a test aid) polls no word a second time.
+constexpr unsigned kSpinLimit = 1u << 20;
+
 // Workspace: a kHeaderBytes header (launch epoch, fault word, completion
 // counters), then the look-back words, then (TTT and backward) per-tile
 // partials.
 constexpr size_t kHeaderBytes = 2048;
+// Header bytes kept when a known workspace changes layout (the launch epoch
+// and the fault word; the completion counters from this offset on are
+// cleared with the look-back words).
+constexpr size_t kHeaderKeepBytes = 64;
 
 struct FwdParams {
   const void* x;
@@ -125,6 +136,7 @@ struct FwdParams {
   unsigned* hdr;               // WsHeader
   float* partials;             // TTT per-tile partials (TTT kernels only)
   float* mono_tab;             // TTT: scaled monomial coefficients [n_lb][KP][64], formed once per launch
+  const unsigned* mono_form;   // TTT: [n_lb] 1 where mono_tab holds Chebyshev coefficients instead
   int64_t x_sb, x_ss, o_sb, o_ss;
   int64_t c_sb, c_sh, c_sk;
   int64_t g_sb, g_ss, g_sh;
@@ -139,6 +151,8 @@ struct FwdParams {
   int clamp_out;
   int nan_zero_u;              // NaN x counts as u = 0 (else z = 0)
   int jitter;                  // OSM_FLAG_TIMING_JITTER: pseudo-random delays (test aid)
+  unsigned poll_limit;         // look-back polls before a wait gives up: kSpinLimit, or 0 under
+                               // OSM_FLAG_POLL_LIMIT_ZERO (test aid)
   float ttt_scale;             // 2 / (B*(S-1)*D)
   int ttt_target;
 };

@@ -112,9 +112,27 @@ __device__ __forceinline__ MonoLoad<KP, G> mono_issue(const FwdParams& p, const 
   return m;
 }
 
+// Which form a tile evaluates its series in.  The monomial form (Horner, K-1
+// FMAs) is exact in exact arithmetic, but its coefficients cancel: its fp32
+// error grows with sum_j |a_j| (a_j scaled as stored, in exp2 units), about
+// ten times faster than Clenshaw's with the size of the Chebyshev
+// coefficients.  A tile uses the monomial form while every scaled monomial
+// coefficient of its lanes satisfies |a_j| <= kMonoBound (NaN counts as
+// above), else the Chebyshev form (Clenshaw, 2(K-1) operations) on c_k
+// scaled the same way.  The bound keeps every draw of the benchmark's
+// c_k ~ N(0, 1/(k+1)^2) (largest |a_j|, a_5 = 2 log2(e) (16 c_5 - 112 c_7),
+// has a standard deviation of 41) and every coefficient set inside the
+// full path's Lion bound 8.31/(k+1)^1.5 (|a_5| <= 145) on Horner, and
+// sends coefficients of order one and larger (c_k ~ N(0, 1): |a_5| ~ 330)
+// to Clenshaw.
+constexpr float kMonoBound = 256.0f;
+
+// mono_store writes coefficient j of every unit; with KP <= kMonoMaxK it
+// also writes, per unit, whether one of its 64 values exceeds kMonoBound
+// (`big`, one word per unit, read after the next barrier by tile_cheb).
 template <int KP, class G>
 __device__ __forceinline__ void mono_store(const MonoLoad<KP, G>& m, const ThreadPos& q,
-                                           float (&mono)[KP][G::LANES]) {
+                                           float (&mono)[KP][G::LANES], unsigned (&big)[KP * G::NSUB]) {
 #pragma unroll
   for (int n = 0; n < m.NJ; ++n) {
     const int u = m.w + n * G::WAVES;
@@ -136,8 +154,46 @@ __device__ __forceinline__ void mono_store(const MonoLoad<KP, G>& m, const Threa
           default: acc = mono_coef<7>(m.cm[n]); break;
         }
       }
-      mono[j][(u % G::NSUB) * kLanes + q.wl] = (float)(acc * (double)m.kap[n]);
+      const float v = (float)(acc * (double)m.kap[n]);
+      mono[j][(u % G::NSUB) * kLanes + q.wl] = v;
+      if constexpr (KP <= kMonoMaxK) {
+        const bool over = __ballot(!(__builtin_fabsf(v) <= kMonoBound)) != 0;
+        if (q.wl == 0) big[u] = over ? 1u : 0u;
+      }
     }
+  }
+}
+
+// True when the tile evaluates the Chebyshev form (uniform over the tile):
+// always above kMonoMaxK coefficients, else when a unit's flag is set.
+template <int KP, class G>
+__device__ __forceinline__ bool tile_cheb(const unsigned (&big)[KP * G::NSUB]) {
+  if constexpr (KP > kMonoMaxK) return true;
+  unsigned f = 0;
+#pragma unroll
+  for (int u = 0; u < KP * G::NSUB; ++u) f |= big[u];
+  return __builtin_amdgcn_readfirstlane(f) != 0;
+}
+
+// The Chebyshev form of a tile's coefficients in place of the monomial one
+// (tiles that tile_cheb sends to Clenshaw): unit (j, sub-block) holds
+// c_j times 2 log2(e) damping_h, rounded once, as mono_store forms it above
+// kMonoMaxK coefficients.  Loads c_j again (a rare path); the caller orders
+// the writes before mono_read with a barrier.
+template <int KP, class G>
+__device__ __forceinline__ void mono_store_cheb(const FwdParams& p, const ThreadPos& q, const TileInfo& ti,
+                                                const TileAddr& a, float (&mono)[KP][G::LANES]) {
+  constexpr int NU = KP * G::NSUB;
+  const int w = __builtin_amdgcn_readfirstlane(q.wave);
+  for (int u = w; u < NU; u += G::WAVES) {
+    const int j = u / G::NSUB;
+    const int d = ti.lbd * G::LANES + (u % G::NSUB) * kLanes + q.wl;
+    const bool ok = d < p.D;
+    const int h = ok ? div_hd(d, p) : 0;
+    const uint32_t vc = ok && j < p.K ? (uint32_t)(((int64_t)h * p.c_sh + (d - h * p.hd)) * 4) : kOffOOB;
+    float v[1];
+    BufVec<float, 1>::load(a.c, vc, (uint32_t)j * a.sc, v);
+    mono[j][(u % G::NSUB) * kLanes + q.wl] = (float)((double)v[0] * (double)(kTwoLog2e * p.damping[h]));
   }
 }
 

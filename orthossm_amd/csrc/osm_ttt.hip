@@ -260,7 +260,8 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   __shared__ float sh_pw[2][kLanes];        // static lambda: run and tile decay of each lane
   // u of every element of the tile (pass 1 -> pass 2 of the same wave), then
   // the per-wave gradient sums (after the barrier that follows pass 2).
-  __shared__ union {
+  // (16-byte aligned: pass 1 and pass 2 move u as f32x4)
+  __shared__ union __attribute__((aligned(16))) {
     float u[NTG][G::LANES][R];   // [token group][lane][token of the run]
     float red[G::WAVES][2 * KP][kLanes];
   } sh_ur;
@@ -277,6 +278,8 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   // lanes), formed once per launch by ttt_mono_prep; loaded before x.
   static_assert(G::NSUB == 1 && KP <= G::WAVES, "one coefficient per wave");
   const float mono_w = q.wave < KP ? p.mono_tab[((size_t)ti.lb * KP + q.wave) * kLanes + q.wl] : 0.0f;
+  // the form of the table (1: Chebyshev coefficients, see ttt_mono_prep)
+  const bool cheb = __builtin_amdgcn_readfirstlane(p.mono_form[ti.lb]) != 0;
 
   // x rows of the run (raw), g (dynamic lambda), and for the tile's last run
   // the row after the tile (its target y and lambda).
@@ -354,9 +357,11 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   bool bad = false;
 #pragma unroll
   for (int i = 0; i < LPT; ++i) bad |= Bv[i] != Bv[i];
-  if (bad) {
-    // A NaN input: z = 0 there (r = 1/2 gives w = 0), or u = 0 with
-    // nan_zero_u; recompute the aggregate.
+  if (bad || cheb) {
+    // Rare: a NaN input (z = 0 there: r = 1/2 gives w = 0; or u = 0 with
+    // nan_zero_u), or a lane-block whose series is in the Chebyshev form (a
+    // coefficient exceeds kMonoBound: the loop above ran Horner on Chebyshev
+    // coefficients, so r is redone with Clenshaw); recompute the aggregate.
 #pragma unroll
     for (int i = 0; i < LPT; ++i) Bv[i] = 0.0f;
 #pragma unroll
@@ -365,8 +370,12 @@ cheby_ema_ttt_kernel(const FwdParams p) {
 #pragma unroll
       for (int i = 0; i < LPT; ++i) {
         const float x = xr.get(r, i);
-        if (x != x) {
-          const float rv = p.nan_zero_u ? tanh_r(c[i][0]) : 0.5f;
+        if (cheb || x != x) {
+          float rv;
+          if (x == x)
+            rv = tanh_r(clenshaw<KP>(softsign_fast(x), c[i]));
+          else
+            rv = p.nan_zero_u ? tanh_r(cheb ? clenshaw<KP>(0.0f, c[i]) : c[i][0]) : 0.5f;
           rr[r][i] = DYN ? rv : __builtin_fmaf(-2.0f * one_m, rv, one_m);
         }
         const float w = DYN ? __builtin_fmaf(-2.0f * one_m, rr[r][i], one_m) : rr[r][i];
@@ -394,7 +403,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     LookBack<G, DYN> lbk;
     look_back_issue<G, DYN>(lbk, q, ti, ls);
     jitter(p.jitter, tags.epoch, 1);
-    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, a_look, p.hdr);
+    look_back_finish<G, DYN>(lbk, L, q, ti, tags, aggA, aggB, ls, init_c, a_look, p.hdr, p.poll_limit);
   }
 
   float y_after[LPT];
@@ -431,6 +440,12 @@ cheby_ema_ttt_kernel(const FwdParams p) {
                    ? p.ema_final + (int64_t)ti.b * p.D + ti.lbd * kLanes + q.lt * LPT
                    : nullptr;
   const float om2 = (1.0f - lam_h) * (1.0f - lam_h);
+  // A NaN state at the run start (a look-back wait that gave up, or a NaN
+  // ema_init) makes every later state of the run NaN; the slow pass 2 takes
+  // it, and its output and gradient terms are replaced by NaN below.
+  bool nan_s = false;
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) nan_s |= s[i] != s[i];
   RunGrad<KP, LPT> rg;
   if (bad || big || ti.is_last)
     ttt_pass2<G, DYN, SOFT, true, XT, OT, KP>(rg, s, xr, ul, rr, lamv, om2, y_after, a, lo, hi, t_first, p.S,
@@ -438,6 +453,27 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   else
     ttt_pass2<G, DYN, SOFT, false, XT, OT, KP>(rg, s, xr, ul, rr, lamv, om2, y_after, a, lo, hi, t_first,
                                                 p.S, clamp, false, fin);
+
+  if (nan_s) {
+    // The clamp (v_med3_f32) turned the NaN states into bounds: store NaN,
+    // and make this run's gradient terms NaN, so the records and the
+    // gradient are NaN (the float64 definition gives NaN there too).
+    static_assert(LPT == 1, "one lane per thread: the NaN state is the thread's");
+    const float qnan = __builtin_nanf("");
+    uint32_t so = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float o[LPT] = {qnan};
+      BufVec<OT, LPT>::store(a.out, a.vo, so, o);
+      so = next_off(so, a.so);
+    }
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      rg.al[i] = qnan;
+#pragma unroll
+      for (int k = 0; k < KP; ++k) rg.P[k][i] = qnan;
+    }
+  }
 
   // Compose the runs of the tile: rho of run g = Ar_g + Br_g rho_tile.
   const float beta = rg.Lp * lam_after;
@@ -496,8 +532,11 @@ cheby_ema_ttt_kernel(const FwdParams p) {
 // them per tile (mono_issue / mono_store): coefficient j of lane l from
 // c_{j+2i} in float64 with the factors cheb_mono(j, i), times 2 log2(e)
 // damping_h, rounded once.  Thread (j, lane) of block lb; lanes >= D get 0.
+// When one of them exceeds kMonoBound (as the forward decides per tile), the
+// lane-block keeps its Chebyshev coefficients instead (c_j times the same
+// scale, for Clenshaw) and form[lb] = 1, else 0.
 template <int KP>
-__global__ void __launch_bounds__(64 * KP) ttt_mono_prep(const FwdParams p, float* tab) {
+__global__ void __launch_bounds__(64 * KP) ttt_mono_prep(const FwdParams p, float* tab, unsigned* form) {
   const int lb = blockIdx.x, j = threadIdx.x / kLanes, l = threadIdx.x % kLanes;
   const int b = lb / p.n_lbd;
   const int d = (lb - b * p.n_lbd) * kLanes + l;
@@ -524,7 +563,10 @@ __global__ void __launch_bounds__(64 * KP) ttt_mono_prep(const FwdParams p, floa
     case 6: acc = mono_coef<6>(cm); break;
     default: acc = mono_coef<7>(cm); break;
   }
-  tab[((size_t)lb * KP + j) * kLanes + l] = (float)(acc * (double)kap);
+  const float v = (float)(acc * (double)kap);
+  const bool cheb = __syncthreads_or(!(__builtin_fabsf(v) <= kMonoBound)) != 0;
+  tab[((size_t)lb * KP + j) * kLanes + l] = cheb ? (float)((double)cm[0] * (double)kap) : v;
+  if (threadIdx.x == 0) form[lb] = cheb ? 1u : 0u;
 }
 
 // Merge of the records n-1 .. 0 of one lane (record i at base + i * rstride,
@@ -602,7 +644,9 @@ hipError_t launch_all(const FwdParams& p0, float* grad, hipStream_t stream) {
   float* chunks = p0.partials + (size_t)p0.n_lb * p0.n_tiles * n_fields<KP>() * kLanes;
   FwdParams p = p0;
   p.mono_tab = chunks + (size_t)p.n_lb * n_chunks * n_fields<KP>() * kLanes;
-  hipLaunchKernelGGL((ttt_mono_prep<KP>), dim3(p.n_lb), dim3(64 * KP), 0, stream, p, p.mono_tab);
+  unsigned* form = reinterpret_cast<unsigned*>(p.mono_tab + (size_t)p.n_lb * KP * kLanes);
+  p.mono_form = form;
+  hipLaunchKernelGGL((ttt_mono_prep<KP>), dim3(p.n_lb), dim3(64 * KP), 0, stream, p, p.mono_tab, form);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const unsigned grid = (unsigned)p.n_lb_pad * (unsigned)p.n_tiles;
@@ -651,8 +695,9 @@ size_t ttt_workspace_bytes(int n_lb, int n_tiles, bool dyn, int K) {
   const size_t F = 2 * kpad + 2;
   const size_t n_chunks = (n_tiles + kChunk - 1) / kChunk;
   const size_t slots = (fwd_workspace_bytes(n_lb, n_tiles, TttTile::LANES, dyn) + 255) / 256 * 256;
-  // per-tile partials, per-chunk merges, the monomial table
-  return slots + (((size_t)n_lb * n_tiles + (size_t)n_lb * n_chunks) * F + (size_t)n_lb * kpad) * kLanes * sizeof(float);
+  // per-tile partials, per-chunk merges, the coefficient table and its form words
+  return slots + (((size_t)n_lb * n_tiles + (size_t)n_lb * n_chunks) * F + (size_t)n_lb * kpad) * kLanes * sizeof(float) +
+         (size_t)n_lb * sizeof(unsigned);
 }
 
 hipError_t launch_ttt(const FwdParams& p, float* grad, int x_dtype, int out_dtype, bool dyn, int tile, int kpad,

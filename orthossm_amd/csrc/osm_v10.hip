@@ -82,10 +82,11 @@ __device__ __forceinline__ float sum_runs(float v) {
   return __uint_as_float(b.x) + __uint_as_float(b.y);
 }
 
+// 16-byte aligned: LUT rows are read as f32x4.
 template <int LW>
-struct V10Lds {
+struct __attribute__((aligned(16))) V10Lds {
   static constexpr int NW = kV10Groups * LW / 64;   // waves per workgroup
-  float lut[256][kLutStride];        // T_k at the table's grid, k contiguous
+  float lut[256][kLutStride];        // T_k at the table's grid, k contiguous (rows 48 bytes apart)
   float cs[8][LW];                   // coefficients of the current chunk
   float ms[8][LW];                   // Lion momentum
   float wA[NW][LW], wB[NW][LW];      // each wave's composed EMA map over its runs

@@ -53,17 +53,41 @@ def set_timing_jitter(on: bool) -> bool:
     return old
 
 
+# Test aid: with the poll limit at zero, the forward, TTT and backward
+# launches carry OSM_FLAG_POLL_LIMIT_ZERO: a look-back wait whose word is not
+# yet published gives up at once (the fault word is set and the outputs that
+# depend on the missing value are NaN), as a wait that passes its poll limit
+# does.
+_poll_limit_zero = False
+
+
+def set_poll_limit_zero(on: bool) -> bool:
+    """Turns OSM_FLAG_POLL_LIMIT_ZERO on or off for later launches; returns the old setting."""
+    global _poll_limit_zero
+    old, _poll_limit_zero = _poll_limit_zero, bool(on)
+    return old
+
+
 def workspace_status(ws: torch.Tensor, *, reset: bool = False, stream: int | None = None) -> tuple[int, int]:
     """(fault word, launch counter) of a workspace, read on ``stream`` (the
     current stream of its device by default) through osm_workspace_status;
     synchronises the host.  A non-zero fault word is the fault tag of the
     last launch whose look-back wait gave up; ``reset`` clears it."""
     lib = nat.load()
+    cur = _current_stream(ws.device)
     if stream is None:
-        stream = torch.cuda.current_stream(ws.device).cuda_stream
+        stream = cur
+    # The status buffer is allocated on the current stream.  When the status
+    # kernel runs on another stream, the current stream is drained first (its
+    # earlier work may still use that memory) and the other stream after the
+    # launch, so the read-back sees the kernel's values.
     st = torch.empty(2, dtype=torch.int32, device=ws.device)
+    if stream != cur:
+        torch.cuda.current_stream(ws.device).synchronize()
     nat.check(lib.osm_workspace_status(ctypes.c_void_p(ws.data_ptr()), ctypes.c_void_p(st.data_ptr()),
                                        1 if reset else 0, ctypes.c_void_p(stream)))
+    if stream != cur:
+        torch.cuda.ExternalStream(stream, device=ws.device).synchronize()
     fault, epoch = (int(v) & 0xFFFFFFFF for v in st.cpu().tolist())
     return fault, epoch
 
@@ -187,7 +211,8 @@ def _prepare(x, coeffs, damping, lam, g, lam_shift, lam_min, lam_max, ema_init, 
     if nan_policy not in ("zero_z", "zero_u"):
         raise ValueError("nan_policy must be 'zero_z' or 'zero_u'")
     a.flags = ((0 if clamp else nat.FLAG_NO_CLAMP) | (nat.FLAG_NAN_ZERO_U if nan_policy == "zero_u" else 0) |
-               (nat.FLAG_TIMING_JITTER if _timing_jitter else 0))
+               (nat.FLAG_TIMING_JITTER if _timing_jitter else 0) |
+               (nat.FLAG_POLL_LIMIT_ZERO if _poll_limit_zero else 0))
     a.B, a.S, a.H, a.hd, a.K = B, S, H, hd, K
     a.x, a.x_dtype, a.x_stride_b, a.x_stride_s = x.data_ptr(), _dtype_code(x.dtype), x.stride(0), x.stride(1)
     a.out_dtype = _dtype_code(odt)

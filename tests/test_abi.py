@@ -94,8 +94,9 @@ def test_ttt_workspace_bytes_formula():
     """TTT: the forward's header and look-back words for 192-token tiles of
     64 lanes (one word per lane, static lambda), 256-byte aligned, then per
     lane 2K+2 floats per tile (the tile records) and per chunk of 16 tiles
-    (their merges), then K floats per lane (the per-launch monomial
-    coefficients), with K padded to 4 or 8."""
+    (their merges), then K floats per lane (the per-launch coefficient
+    table), with K padded to 4 or 8, then one word per lane-block (the
+    table's form: monomial or Chebyshev)."""
     lib = nat.load()
     a = _args()
     n_lb, n_tiles = 4 * 8, -(-16384 // 192)
@@ -104,7 +105,7 @@ def test_ttt_workspace_bytes_formula():
     def want(kpad, words):
         slots = 2048 + n_lb * n_tiles * 64 * 8 * words
         slots = -(-slots // 256) * 256
-        return slots + ((n_lb * n_tiles + n_lb * n_chunks) * (2 * kpad + 2) + n_lb * kpad) * 64 * 4
+        return slots + ((n_lb * n_tiles + n_lb * n_chunks) * (2 * kpad + 2) + n_lb * kpad) * 64 * 4 + n_lb * 4
 
     assert lib.osm_workspace_bytes(ctypes.byref(a), 1) == want(8, 1)
     a.K = 3

@@ -2,13 +2,17 @@
 after ordinary launches, a launch counter that grows by one per launch and
 keeps growing across a layout change, and a fault left by an earlier launch
 (planted from the host into the header) that is reported, that raises under
-the per-launch check, and that does not disturb later launches."""
+the per-launch check, and that does not disturb later launches; and a
+launch whose look-back waits give up (forced from the host with
+OSM_FLAG_POLL_LIMIT_ZERO), which leaves NaN in the outputs that depend on
+the lost values instead of plausible numbers."""
+import numpy as np
 import pytest
 import torch
 
 from helpers import assert_close_fp32, inputs, oracle_forward, to_dev
 from orthossm_amd import _native as nat
-from orthossm_amd import cheby_ema_forward, ops
+from orthossm_amd import cheby_ema_backward, cheby_ema_forward, cheby_ema_ttt, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -74,3 +78,89 @@ def test_status_argument_errors(dev):
     assert lib.osm_workspace_status(ctypes.c_void_p(ws.data_ptr() + 4), ctypes.c_void_p(st.data_ptr()), 0,
                                     None) == -5
     assert lib.osm_workspace_status(ctypes.c_void_p(ws.data_ptr()), None, 0, None) == -1
+
+
+def _equal_or_nan(got, want, what):
+    """Every element of `got` is NaN or bit-equal to `want`; returns the NaN mask."""
+    g = got.float().cpu().numpy()
+    w = want.float().cpu().numpy()
+    nan = np.isnan(g)
+    assert not np.isnan(w).any(), f"{what}: the reference launch has NaN"
+    assert np.array_equal(g[~nan].view(np.uint32), w[~nan].view(np.uint32)), \
+        f"{what}: an element that is not NaN differs from the normal launch"
+    return nan
+
+
+def _run_case(case, d, dev):
+    """One launch of `case`; returns (tensors, workspace op)."""
+    if case == "fwd_static":
+        out, fin = cheby_ema_forward(d["x"], d["coeffs"], d["damping"], d["lam"], return_state=True)
+        return (out, fin), nat.OP_FWD
+    if case == "fwd_dynamic":
+        out, fin = cheby_ema_forward(d["x"], d["coeffs"], d["damping"], d["lam"], g=d["g"], return_state=True)
+        return (out, fin), nat.OP_FWD
+    if case == "ttt":
+        out, grad = cheby_ema_ttt(d["x"], d["coeffs"], d["damping"], d["lam"], g=d.get("g"))
+        return (out, grad), nat.OP_TTT
+    out = d["out_saved"]
+    gx, gc, gi = cheby_ema_backward(d["x"], d["coeffs"], d["damping"], d["lam"], out, d["go"], need_init=True)
+    return (gx, gc, gi), nat.OP_BWD
+
+
+@pytest.mark.parametrize("case", ["fwd_static", "fwd_dynamic", "ttt", "bwd"])
+def test_poll_limit_zero_poisons_the_dependent_outputs(dev, case):
+    """OSM_FLAG_POLL_LIMIT_ZERO (with the timing jitter, so that tiles
+    publish late): a look-back word not yet published at its first read
+    gives up at once, as a wait past its poll limit does.  Every kernel
+    exits; the fault word holds the launch's fault tag; each output element
+    is NaN or bit-equal to a normal launch's (outputs downstream of a lost
+    carry are NaN, the rest unaffected); the next normal launch is clean."""
+    dyn = case == "fwd_dynamic"
+    B, S = (2, 40000) if case.startswith("fwd") else (2, 24000)
+    inp = inputs(B, S, 8, 64, seed=60, dynamic=dyn)
+    d = to_dev(inp, dev)
+    if case == "bwd":
+        d["out_saved"] = cheby_ema_forward(d["x"], d["coeffs"], d["damping"], d["lam"])
+        d["go"] = torch.randn(B, S, 512, generator=torch.Generator().manual_seed(61)).to(dev)
+    ref, op = _run_case(case, d, dev)
+    ref = [t.clone() for t in ref]
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    ws = ops._ws_cache[(dev.index, stream, op)]
+    assert ops.workspace_status(ws)[0] == 0
+    old_j, old_p = ops.set_timing_jitter(True), ops.set_poll_limit_zero(True)
+    try:
+        # a give-up depends on timing: up to four launches until one happens
+        for _ in range(4):
+            _, epoch = ops.workspace_status(ws)
+            got, _ = _run_case(case, d, dev)
+            fault, _ = ops.workspace_status(ws, reset=True)
+            if fault:
+                break
+    finally:
+        ops.set_timing_jitter(old_j)
+        ops.set_poll_limit_zero(old_p)
+    assert fault == (((epoch & 0x3FFFFFFF) << 2) | 3), f"fault word {fault:#x} after launch {epoch}"
+    masks = [_equal_or_nan(g, w, f"{case}[{i}]") for i, (g, w) in enumerate(zip(got, ref))]
+    assert masks[0].any(), "the fault word is set but no output is NaN"
+    print(f"{case}: {masks[0].mean():.4f} of the first output NaN", flush=True)
+    # the next launch is clean and equal to the normal one
+    again, _ = _run_case(case, d, dev)
+    for i, (g, w) in enumerate(zip(again, ref)):
+        assert torch.equal(g, w), f"{case}[{i}] after the poisoned launch"
+    assert ops.workspace_status(ws)[0] == 0
+
+
+def test_status_read_on_another_stream(dev):
+    """workspace_status(stream=...) for a workspace used on a side stream,
+    called while the default stream is current: the counter it returns
+    counts every launch made on that stream."""
+    inp = to_dev(inputs(1, 3000, 8, 64, seed=62), dev)
+    side = torch.cuda.Stream(dev)
+    with torch.cuda.stream(side):
+        cheby_ema_forward(inp["x"], inp["coeffs"], inp["damping"], inp["lam"])
+    ws = ops._ws_cache[(dev.index, side.cuda_stream, nat.OP_FWD)]
+    _, e0 = ops.workspace_status(ws, stream=side.cuda_stream)
+    with torch.cuda.stream(side):
+        for _ in range(5):
+            cheby_ema_forward(inp["x"], inp["coeffs"], inp["damping"], inp["lam"])
+    assert ops.workspace_status(ws, stream=side.cuda_stream) == (0, e0 + 5)
