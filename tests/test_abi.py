@@ -90,6 +90,20 @@ def test_workspace_bytes_formula():
     assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 0
 
 
+def test_workspace_bytes_without_pointers():
+    """A shapes-only forward query with x or out NULL does not know their
+    alignment and is sized for the one-lane geometry (128-token tiles), the
+    largest: a later call with rows off 4-element boundaries (which takes
+    that geometry) fits the workspace so sized."""
+    lib = nat.load()
+    one_lane = 2048 + 32 * 128 * 64 * 8
+    assert lib.osm_workspace_bytes(ctypes.byref(_args(x=0, out=0)), 0) == one_lane
+    assert lib.osm_workspace_bytes(ctypes.byref(_args(out=0)), 0) == one_lane
+    # a view one element off the 4-element boundary asks for the same size
+    assert lib.osm_workspace_bytes(ctypes.byref(_args(x=0x10004)), 0) == one_lane
+    assert lib.osm_workspace_bytes(ctypes.byref(_args()), 0) == 2048 + 32 * 32 * 64 * 8
+
+
 def test_ttt_workspace_bytes_formula():
     """TTT: the forward's header and look-back words for 192-token tiles of
     64 lanes (one word per lane, static lambda), 256-byte aligned, then per
@@ -116,13 +130,14 @@ def test_ttt_workspace_bytes_formula():
 
 def test_flag_values_match_the_header():
     text = open(os.path.join(ROOT, "include", "osm.h")).read()
-    for name in ("NO_CLAMP", "NAN_ZERO_U", "FULL_JACOBIAN", "TIMING_JITTER"):
+    for name in ("NO_CLAMP", "NAN_ZERO_U", "FULL_JACOBIAN", "TIMING_JITTER", "POLL_LIMIT_ZERO"):
         m = re.search(rf"#define OSM_FLAG_{name} (0x[0-9a-fA-F]+)", text)
         assert m and int(m.group(1), 16) == getattr(nat, f"FLAG_{name}"), name
     lib = nat.load()
-    # the timing-jitter test aid is accepted by the forward, TTT and backward
+    # the test aids are accepted by the forward, TTT and backward
     for op in (nat.OP_FWD, nat.OP_TTT, nat.OP_BWD):
-        assert lib.osm_workspace_bytes(ctypes.byref(_args(flags=nat.FLAG_TIMING_JITTER)), op) > 0
+        for flag in (nat.FLAG_TIMING_JITTER, nat.FLAG_POLL_LIMIT_ZERO):
+            assert lib.osm_workspace_bytes(ctypes.byref(_args(flags=flag)), op) > 0
 
 
 def test_coefficient_limits_per_entry_point():
@@ -209,6 +224,7 @@ def _bwd(**kw):
     (dict(out=0), {}, -1),                    # the clamp mask needs the saved output
     (dict(out=0, flags=nat.FLAG_NO_CLAMP), {}, -5),   # ... unless there is no clamp: reaches the workspace check
     (dict(K=17), {}, -2),
+    (dict(K=9), dict(z_saved=0x20000, z_stride_b=16384 * 512, z_stride_s=512), -1),   # the saved z needs K <= 8
 ])
 def test_bwd_argument_errors(akw, bkw, code):
     lib = nat.load()

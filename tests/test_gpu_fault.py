@@ -164,3 +164,27 @@ def test_status_read_on_another_stream(dev):
         for _ in range(5):
             cheby_ema_forward(inp["x"], inp["coeffs"], inp["damping"], inp["lam"])
     assert ops.workspace_status(ws, stream=side.cuda_stream) == (0, e0 + 5)
+
+
+def test_layout_change_repairs_stale_counters(dev):
+    """Completion counters left non-zero in the header (what two calls that
+    overlap on one workspace, a misuse, can leave) are cleared by the next
+    layout change, which keeps the launch counter and the fault word: later
+    launches count correctly and match the oracle."""
+    a = to_dev(inputs(2, 5000, 8, 64, seed=63), dev)
+    b_in = inputs(1, 7000, 8, 64, seed=64)
+    b = to_dev(b_in, dev)
+    cheby_ema_forward(a["x"], a["coeffs"], a["damping"], a["lam"])
+    ws = _fwd_ws(dev)
+    _, e0 = ops.workspace_status(ws)
+    torch.cuda.synchronize()
+    words = ws.view(torch.int32)
+    words[16] = 3                       # done_all (byte 64)
+    for c in range(8):
+        words[32 + 32 * c] = 5 + c      # cls[c].done (byte 128 + 128 c)
+    torch.cuda.synchronize()
+    # another layout: its clear zeroes the counters
+    for i in range(3):
+        got = cheby_ema_forward(b["x"], b["coeffs"], b["damping"], b["lam"])
+    assert ops.workspace_status(ws) == (0, e0 + 3)
+    assert_close_fp32(got.cpu().numpy(), oracle_forward(b_in)[0])

@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close_fp32, inputs, oracle_forward, to_dev
+from helpers import assert_close_fp32, inputs, oracle_c_forward_row, oracle_forward, to_dev
 from oracle import cheby_ema as O
 from orthossm_amd import cheby_ema_forward, cheby_ema_ttt
 from orthossm_amd.synthetic import CONFIGS, make_config_inputs
@@ -209,17 +209,18 @@ def test_streaming_config_full_size(dev):
 
 
 def test_dynamic_config_full_size(dev):
-    """B=8 S=32768 D=1024 dynamic lambda.  The kernel runs at full
-    size; batches 0 and 7 are checked against the oracle (each batch row is
-    an independent recurrence)."""
+    """B=8 S=32768 D=1024 dynamic lambda, at full size: every
+    batch row (each an independent recurrence) is checked against the
+    float64 oracle's C restatement (oracle/cheby_ema_c.c, pinned against the
+    numpy oracle on the CPU), out and ema_final.  Measured on one MI355X box
+    (16 host cores): 4.0 s for the test, all eight rows included."""
     inp = make_config_inputs(CONFIGS["dynamic"])
     out, fin = run(inp, dev, return_state=True)
     out, fin = out.cpu(), fin.cpu()
-    for b in (0, 7):
-        sub = {k: (v[b:b + 1] if k in ("x", "coeffs", "g") else v) for k, v in inp.items()}
-        want, wfin = oracle_forward(sub)
-        assert_close_fp32(out[b:b + 1], want)
-        assert_close_fp32(fin[b:b + 1], wfin, what="ema_final")
+    for b in range(CONFIGS["dynamic"].B):
+        want, wfin = oracle_c_forward_row(inp, b)
+        assert_close_fp32(out[b], want, what=f"out row {b}")
+        assert_close_fp32(fin[b], wfin, what=f"ema_final row {b}")
 
 
 def test_drop_in_fast_path_matches_oracle(dev):

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close_fp32, inputs, oracle_forward, oracle_ttt, to_dev
+from helpers import assert_close_fp32, inputs, oracle_c_ttt_row, oracle_forward, oracle_ttt, to_dev
 from oracle import cheby_ema as O
 from orthossm_amd import cheby_ema_forward, cheby_ema_ttt
 from orthossm_amd.synthetic import CONFIGS, make_config_inputs
@@ -130,19 +130,23 @@ def test_ttt_deterministic(dev):
 
 
 def test_bf16_ttt_config_full_size(dev):
-    """B=16 S=65536 D=512, bf16 I/O, fp32 state, fused TTT.  The
-    kernel runs at full size; the first and the last batch row (0 and 15) are
-    each compared with the oracle run on that row alone (the MSE mean over B
-    rows scales a row's gradient by 1/B)."""
+    """B=16 S=65536 D=512, bf16 I/O, fp32 state, fused TTT, at
+    full size: every batch row is compared with the float64 oracle's C
+    restatement (oracle/cheby_ema_c.c, pinned against the numpy oracle on the
+    CPU) run on that row with the loss mean over the whole batch: out (bf16,
+    2e-2), ema_final (fp32) and the gradient (1e-3).  Measured on one MI355X
+    box (16 host cores): 5.1 s for the test, all sixteen rows included."""
     cfg = CONFIGS["bf16_ttt"]
     inp = make_config_inputs(cfg)
-    out, grad = run(inp, dev)
-    for b in (0, cfg.B - 1):
-        sub = {k: (v[b:b + 1] if k in ("x", "coeffs") else v) for k, v in inp.items()}
-        G, want, _ = oracle_ttt(sub)
-        err = np.abs(out[b:b + 1].float().cpu().numpy() - want)
+    out, grad, fin = run(inp, dev, return_state=True)
+    out, grad, fin = out.float().cpu().numpy(), grad.cpu(), fin.cpu()
+    n_total = cfg.B * (cfg.S - 1) * cfg.D
+    for b in range(cfg.B):
+        G, want, wfin = oracle_c_ttt_row(inp, b, n_total=n_total)
+        err = np.abs(out[b] - want)
         assert err.max() <= 2e-2, f"row {b}: out error {err.max():.3e}"
-        assert_grad(grad[b:b + 1] * cfg.B, G)
+        assert_close_fp32(fin[b], wfin, what=f"ema_final row {b}")
+        assert_grad(grad[b:b + 1], G[None])
 
 
 @pytest.mark.parametrize("source", ["lion", "bound"])
