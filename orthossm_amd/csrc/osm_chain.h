@@ -17,11 +17,12 @@
 // sb*WPS .. sb*WPS+WPS-1, each reading WPT predecessor tiles, so that
 // CKPT = WPS * WPT.  Look-back words are laid out [lane-block][tile][lane].
 //
-// Tile order.  Virtual tile v covers tile v / n_lb_pad of lane-block
-// v % n_lb_pad, with n_lb_pad = n_lb rounded up to a multiple of 8 (virtual
-// tiles with lane-block >= n_lb are padding and are skipped).  A tile waits
-// only on earlier tiles of its lane-block: v - k*n_lb_pad, the same class
-// v % 8.  Block b handles v = b.  Awaited blocks have a lower index at a
+// Tile order.  Virtual tile v covers tile v / n_lb_pad of the lane-block in
+// slot v % n_lb_pad, with n_lb_pad = n_lb rounded up to a multiple of 8
+// (tile_info maps slots to lane-blocks so that consecutive lane-blocks share
+// a class; virtual tiles with lane-block >= n_lb are padding and are
+// skipped).  A tile waits only on earlier tiles of its lane-block:
+// v - k*n_lb_pad, the same slot and class v % 8.  Block b handles v = b.  Awaited blocks have a lower index at a
 // stride that is a multiple of 8; workgroups go to the 8 XCDs round-robin by
 // index and in index order within an XCD, so each awaited block sits on the
 // same XCD and was dispatched before the waiter.  The waits are bounded
@@ -96,7 +97,13 @@ __device__ __forceinline__ TileInfo tile_info(int v, int n_lb, int n_lb_pad, int
   TileInfo ti;
   ti.v = v;
   ti.tile = v / n_lb_pad;
-  ti.lb = v - ti.tile * n_lb_pad;
+  // Slot s = v mod n_lb_pad (XCD class s mod 8) serves lane-block
+  // (s mod 8) * m + s / 8, m = n_lb_pad / 8: the m consecutive lane-blocks
+  // c m .. c m + m - 1 all belong to class c, so the lane-blocks of a batch
+  // row share one XCD and its L2 (they read the same lines of g, one value
+  // per head per token), and every class still holds m lane-blocks.
+  const int s = v - ti.tile * n_lb_pad;
+  ti.lb = (s & 7) * (n_lb_pad >> 3) + (s >> 3);
   ti.pad = ti.lb >= n_lb;
   ti.b = ti.lb / n_lbd;
   ti.lbd = ti.lb - ti.b * n_lbd;

@@ -23,6 +23,22 @@
 namespace osm {
 namespace {
 
+// lambda of the tokens of a thread's run: lam[r] for r < R.  Static: the
+// head's lambda.  Dynamic: a row of the tile's per-token lambda in LDS
+// (formed once per token and head by the workgroup, see the kernel).
+template <bool DYN>
+struct RunLam;
+template <>
+struct RunLam<false> {
+  float lam;
+  __device__ __forceinline__ float operator[](int) const { return lam; }
+};
+template <>
+struct RunLam<true> {
+  const float* row;
+  __device__ __forceinline__ float operator[](int r) const { return row[r]; }
+};
+
 // Exact input for the rare path (see pass1_exact): +-Inf -> u = +-1; NaN x
 // -> w = 0 as sdpc_kernel.py:2086, or (nan_zero_u) u = 0 as
 // sdpc_kernel.py:1725.
@@ -41,7 +57,7 @@ __device__ __forceinline__ float ema_input_exact(float x, const float (&a)[KP], 
 // special-value handling, in the series form of the tile (cheb: Clenshaw).
 template <class G, bool DYN, typename XT, int KP>
 __device__ __forceinline__ void pass1_exact(float (&w)[G::R][G::LPT], const TileAddr& a, const float (&c)[G::LPT][KP],
-                                            const float (&lamv)[G::R], float (&Bv)[G::LPT], bool nan_zero_u,
+                                            const RunLam<DYN>& lamv, float (&Bv)[G::LPT], bool nan_zero_u,
                                             bool cheb) {
 #pragma unroll
   for (int i = 0; i < G::LPT; ++i) Bv[i] = 0.0f;
@@ -57,6 +73,9 @@ __device__ __forceinline__ void pass1_exact(float (&w)[G::R][G::LPT], const Tile
       w[r][i] = ema_input_exact<KP>(xv[i], c[i], one_m, n2, nan_zero_u, cheb);
       Bv[i] = __builtin_fmaf(lam, Bv[i], w[r][i]);
     }
+    // one row at a time: the scheduler would otherwise issue every row's
+    // reload first and hold them beside w (spills with a dynamic lambda)
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -65,8 +84,8 @@ __device__ __forceinline__ void pass1_exact(float (&w)[G::R][G::LPT], const Tile
 // (when fin is non-NULL).  NANP: a NaN state is stored as NaN (the clamp,
 // v_med3_f32, would return a bound); taken when the carried state is NaN,
 // which a look-back wait that gave up leaves (or a NaN ema_init).
-template <class G, typename OT, bool FINAL, bool NANP>
-__device__ __forceinline__ void pass2(float (&s)[G::LPT], const float (&w)[G::R][G::LPT], const float (&lamv)[G::R],
+template <class G, bool DYN, typename OT, bool FINAL, bool NANP>
+__device__ __forceinline__ void pass2(float (&s)[G::LPT], const float (&w)[G::R][G::LPT], const RunLam<DYN>& lamv,
                                       const TileAddr& a, float lo, float hi, int r_fin, float* fin) {
   uint32_t so = 0;
 #pragma unroll
@@ -126,21 +145,48 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     }
   }
   const float lam_h = p.lam[a.h];
-  float lamv[R];
+  // Dynamic lambda: the workgroup loads g for the tile's tokens and the
+  // heads its lanes span (one value per token and head, not one per thread)
+  // and forms lambda = clamp(lam_h + lam_shift g) once into LDS,
+  // lam_s[head - h0][token]; threads read their run's row from there in
+  // both passes instead of holding R values in registers.
+  constexpr int NHB = DYN ? (LPT == 1 ? G::LANES : G::LANES / 4) : 1;   // heads a lane-block can span
+  constexpr int kGL = 2;   // g loads per thread held in registers (the rest: a rare loop)
+  __shared__ float lam_s[NHB][DYN ? G::TILE : 1];
+  int h0 = 0, n_gl = 0;
+  float glv[kGL];
   if constexpr (DYN) {
-    uint32_t sg = 0;
+    const int d0 = ti.lbd * G::LANES;
+    h0 = div_hd(d0, p);
+    n_gl = (div_hd(min(d0 + G::LANES, p.D) - 1, p) - h0 + 1) * G::TILE;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float gv[1];
-      BufVec<float, 1>::load(a.g, a.vg, sg, gv);
-      lamv[r] = gv[0];
-      sg = next_off(sg, a.sg);
+    for (int i = 0; i < kGL; ++i) {
+      const int idx = q.tid + i * G::THREADS;
+      const int t = idx % G::TILE, hh = idx / G::TILE;
+      float v[1];
+      BufVec<float, 1>::load(a.g, idx < n_gl ? (uint32_t)((t * p.g_ss + (h0 + hh) * p.g_sh) * 4) : kOffOOB, 0, v);
+      glv[i] = v[0];
     }
   }
 
   __builtin_amdgcn_s_setprio(0);
   __shared__ unsigned mono_big[KP * G::NSUB];
   mono_store<KP, G>(ml, q, mono, mono_big);
+  if constexpr (DYN) {
+    auto lam_of = [&](int idx, float gv) {
+      const int t = idx % G::TILE, hh = idx / G::TILE;
+      lam_s[hh][t] = __builtin_amdgcn_fmed3f(__builtin_fmaf(p.lam_shift, gv, p.lam[h0 + hh]), p.lam_min, p.lam_max);
+    };
+#pragma unroll
+    for (int i = 0; i < kGL; ++i)
+      if (q.tid + i * G::THREADS < n_gl) lam_of(q.tid + i * G::THREADS, glv[i]);
+    for (int idx = q.tid + kGL * G::THREADS; idx < n_gl; idx += G::THREADS) {   // small heads only
+      float v[1];
+      const int t = idx % G::TILE, hh = idx / G::TILE;
+      BufVec<float, 1>::load(a.g, (uint32_t)((t * p.g_ss + (h0 + hh) * p.g_sh) * 4), 0, v);
+      lam_of(idx, v[0]);
+    }
+  }
   __syncthreads();
   // Monomial form unless a coefficient of the tile exceeds kMonoBound (rare:
   // the Chebyshev coefficients replace the table, one more barrier).
@@ -151,6 +197,11 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   }
   float c[LPT][KP];
   mono_read<G, KP>(mono, q, c);
+  RunLam<DYN> lamv;
+  if constexpr (DYN)
+    lamv.row = &lam_s[min(max(a.h - h0, 0), NHB - 1)][q.tg * R];   // (lanes >= D: any row)
+  else
+    lamv.lam = lam_h;
 
   // Pass 1: w = (1 - lam) * tanh(damping * p(u)) in place of x, and the run
   // aggregate (A, B) from a zero state.  softsign as copysign(1 - 1/(1+|x|), x):
@@ -174,10 +225,6 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     float u[kRB][LPT], py[kRB][LPT];
 #pragma unroll
     for (int rr = 0; rr < kRB; ++rr) {
-      float lam = lam_h;
-      if constexpr (DYN)
-        lam = __builtin_amdgcn_fmed3f(__builtin_fmaf(p.lam_shift, lamv[r0 + rr], lam_h), p.lam_min, p.lam_max);
-      lamv[r0 + rr] = lam;
 #pragma unroll
       for (int i = 0; i < LPT; ++i) {
         u[rr][i] = softsign_fast(w[r0 + rr][i]);
@@ -198,6 +245,10 @@ cheby_ema_fwd_kernel(const FwdParams p) {
 #pragma unroll
           for (int i = 0; i < LPT; ++i) py[rr][i] = __builtin_fmaf(py[rr][i], u[rr][i], c[i][j]);
     }
+    // (dynamic lambda: the row block's lambda is read from LDS here; the
+    // empty asm keeps the compiler from reading the whole run's lambda at
+    // the start of the pass and holding it in registers)
+    if constexpr (DYN) asm volatile("" ::: "memory");
 #pragma unroll
     for (int rr = 0; rr < kRB; ++rr) {
       const float lam = lamv[r0 + rr];
@@ -253,9 +304,9 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   for (int i = 0; i < LPT; ++i) nan_s |= s[i] != s[i];
   if (!ti.is_last) {
     if (!nan_s)
-      pass2<G, OT, false, false>(s, w, lamv, a, lo, hi, 0, nullptr);
+      pass2<G, DYN, OT, false, false>(s, w, lamv, a, lo, hi, 0, nullptr);
     else
-      pass2<G, OT, false, true>(s, w, lamv, a, lo, hi, 0, nullptr);
+      pass2<G, DYN, OT, false, true>(s, w, lamv, a, lo, hi, 0, nullptr);
   } else {
     // The last tile also yields ema_final: the unclamped state at token S-1,
     // from the one run that holds it.
@@ -263,7 +314,7 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     float* fin = (p.ema_final && a.vo != kOffOOB && r_last >= 0 && r_last < R)
                      ? p.ema_final + (int64_t)ti.b * p.D + ti.lbd * G::LANES + q.lt * LPT
                      : nullptr;
-    pass2<G, OT, true, true>(s, w, lamv, a, lo, hi, r_last, fin);
+    pass2<G, DYN, OT, true, true>(s, w, lamv, a, lo, hi, r_last, fin);
   }
 }
 
@@ -304,6 +355,8 @@ hipError_t launch_k(const FwdParams& p, FwdShape s, int kpad, hipStream_t stream
   if (is_shape<FwdTileGeneric>(s)) return launch_generic<DYN, XT, OT>(p, kpad, stream);
   if constexpr (!DYN) {
     if (is_shape<FwdTileLarge>(s)) return launch_g<FwdTileLarge, DYN, XT, OT>(p, kpad, stream);
+  } else {
+    if (is_shape<FwdTileLargeDyn>(s)) return launch_g<FwdTileLargeDyn, DYN, XT, OT>(p, kpad, stream);
   }
   if (is_shape<FwdTileMedium>(s)) return launch_g<FwdTileMedium, DYN, XT, OT>(p, kpad, stream);
   if (is_shape<FwdTileSmall>(s)) return launch_g<FwdTileSmall, DYN, XT, OT>(p, kpad, stream);
@@ -351,7 +404,10 @@ FwdShape fwd_geometry(bool dyn, int64_t B, int64_t D, int64_t S, bool generic) {
   // lambda holds more per-token state and is limited to the medium tile.
   constexpr int64_t kMinTiles = 512;
   auto n_work = [&](int tile, int lanes) { return B * ((D + lanes - 1) / lanes) * ((S + tile - 1) / tile); };
-  if (!dyn && n_work(FwdTileLarge::TILE, FwdTileLarge::LANES) >= kMinTiles)
+  static_assert(FwdTileLarge::TILE == FwdTileLargeDyn::TILE && FwdTileLarge::LANES == FwdTileLargeDyn::LANES &&
+                    FwdTileLarge::LPT == FwdTileLargeDyn::LPT,
+                "the static and dynamic large tiles share a shape");
+  if (n_work(FwdTileLarge::TILE, FwdTileLarge::LANES) >= kMinTiles)
     return {FwdTileLarge::TILE, FwdTileLarge::LANES, FwdTileLarge::LPT};
   if (n_work(FwdTileMedium::TILE, FwdTileMedium::LANES) >= kMinTiles)
     return {FwdTileMedium::TILE, FwdTileMedium::LANES, FwdTileMedium::LPT};

@@ -55,6 +55,10 @@ struct TileGeo {
 // 420 us against 429 with two and 449 with eight.  The large tile keeps
 // eight (no difference at configs[1]).
 using FwdTileLarge = TileGeo<2, 8, 32>;           // 512 tokens x 64 lanes
+// Dynamic lambda at 512 tokens: the per-token lambda lives in LDS (formed
+// once per token and head), which leaves the registers for the run; one
+// look-back word per thread (two per word pair: A and B).
+using FwdTileLargeDyn = TileGeo<2, 8, 32, 64, 1>;
 using FwdTileMedium = TileGeo<2, 8, 16, 64, 1>;   // 256 tokens x 64 lanes
 using FwdTileSmall = TileGeo<2, 8, 8, 64, 1>;     // 128 tokens x 64 lanes
 // One lane per thread: any head size, rows aligned to one element, and the

@@ -74,9 +74,9 @@ def test_workspace_bytes_formula():
     # lambda uses 512-token tiles of 64-lane lane-blocks (4 x 8 lane-blocks,
     # 32 tiles each at S=16384)
     assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 32 * 64 * 8
-    # dynamic lambda: 256-token tiles, two words (A and B) per lane
+    # dynamic lambda: the same 512-token tiles, two words (A and B) per lane
     a.g = 0x10000
-    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 64 * 64 * 16
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 32 * 64 * 16
     # more than 8 coefficients, or rows off 4-element boundaries, or a head
     # size that is not a multiple of 4: the one-lane geometry, 128-token tiles
     a.K = 9

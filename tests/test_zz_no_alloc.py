@@ -87,11 +87,11 @@ def test_static_scratch_repeated_same_layout(dev):
 
 def test_static_scratch_refuses_shapes_beyond_its_size(dev):
     lib = nat.load()
-    # dynamic lambda, 64 lanes, 256-token tiles: 8.4e6 tokens need 32813 tiles
+    # dynamic lambda, 64 lanes, 512-token tiles: 1.7e7 tokens need 33204 tiles
     # x 64 lanes x 2 words x 8 bytes > 32 MiB of look-back words.  x and g
     # are broadcast (stride 0); out is real memory, so nothing could go out
     # of bounds even if the size check were missing.
-    S, H, hd = 8_400_000, 1, 64
+    S, H, hd = 17_000_000, 1, 64
     x = torch.randn(1, 1, H * hd, device=dev).to(torch.bfloat16).expand(1, S, H * hd)
     out = torch.empty(1, S, H * hd, device=dev, dtype=torch.bfloat16)
     g = torch.zeros(1, 1, H, device=dev).expand(1, S, H)
