@@ -35,8 +35,11 @@ struct RunLam<false> {
 };
 template <>
 struct RunLam<true> {
-  const float* row;
-  __device__ __forceinline__ float operator[](int r) const { return row[r]; }
+  const float* row;   // 16-byte aligned
+  // four tokens per LDS read (the reads of one quad are shared after unrolling)
+  __device__ __forceinline__ float operator[](int r) const {
+    return reinterpret_cast<const f32x4*>(row)[r >> 2][r & 3];
+  }
 };
 
 // Exact input for the rare path (see pass1_exact): +-Inf -> u = +-1; NaN x
@@ -47,7 +50,11 @@ __device__ __forceinline__ float ema_input_exact(float x, const float (&a)[KP], 
                                                  bool nan_zero_u, bool cheb) {
   const bool ok = x == x;
   const float u = ok ? softsign(x) : 0.0f;
-  const float r = tanh_r(cheb ? series_as<KP, true>(u, a) : series_as<KP, false>(u, a));
+  // both forms, then a select: a branch per element on the tile's form
+  // splits the unrolled rare path into many blocks and costs registers
+  float pc = series_as<KP, true>(u, a), pm = series_as<KP, false>(u, a);
+  asm volatile("" : "+v"(pc), "+v"(pm));
+  const float r = tanh_r(cheb ? pc : pm);
   const float w = __builtin_fmaf(neg2_one_m, r, one_m);
   return (ok || nan_zero_u) ? w : 0.0f;
 }
@@ -152,7 +159,8 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   // both passes instead of holding R values in registers.
   constexpr int NHB = DYN ? (LPT == 1 ? G::LANES : G::LANES / 4) : 1;   // heads a lane-block can span
   constexpr int kGL = 2;   // g loads per thread held in registers (the rest: a rare loop)
-  __shared__ float lam_s[NHB][DYN ? G::TILE : 1];
+  static_assert(!DYN || (R % 4 == 0 && G::TILE % 4 == 0), "runs read lambda four tokens at a time");
+  __shared__ __attribute__((aligned(16))) float lam_s[NHB][DYN ? G::TILE : 1];
   int h0 = 0, n_gl = 0;
   float glv[kGL];
   if constexpr (DYN) {
@@ -245,10 +253,6 @@ cheby_ema_fwd_kernel(const FwdParams p) {
 #pragma unroll
           for (int i = 0; i < LPT; ++i) py[rr][i] = __builtin_fmaf(py[rr][i], u[rr][i], c[i][j]);
     }
-    // (dynamic lambda: the row block's lambda is read from LDS here; the
-    // empty asm keeps the compiler from reading the whole run's lambda at
-    // the start of the pass and holding it in registers)
-    if constexpr (DYN) asm volatile("" ::: "memory");
 #pragma unroll
     for (int rr = 0; rr < kRB; ++rr) {
       const float lam = lamv[r0 + rr];
