@@ -142,6 +142,36 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
   }
   const float gamma = 0.98f - 0.06f * (float)h / (float)p.H;
   const float mu = p.mu_dev ? *p.mu_dev : p.mu, one_m = 1.0f - mu;
+  // Decays of full blocks (every token valid): a run's mu^R as the runs
+  // form it, its powers for the scan steps, and this thread's weights of the
+  // earlier waves' maps.
+  struct {
+    float run_pow[4];                 // ar^(2^j), ar = mu^R
+    float run_lead;                   // ar^gw: runs of this wave before this thread's
+    float wave_pow;                   // aw^wave, aw = ar^GPW
+    float wave_w[V10Lds<LW>::NW];     // aw^(wave-1-q) for q < wave, else 0
+  } kc;
+  {
+    float ar = 1.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) ar *= mu;
+    kc.run_pow[0] = ar;
+#pragma unroll
+    for (int j = 1; j < 4; ++j) kc.run_pow[j] = kc.run_pow[j - 1] * kc.run_pow[j - 1];
+    float aw = 1.0f;
+#pragma unroll
+    for (int gg = 0; gg < GPW; ++gg) aw *= ar;
+    kc.run_lead = 1.0f;
+    for (int gg = 0; gg < gw; ++gg) kc.run_lead *= ar;
+    kc.wave_pow = 1.0f;
+    for (int q = 0; q < wave; ++q) kc.wave_pow *= aw;
+    float pw = 1.0f;
+#pragma unroll
+    for (int q = V10Lds<LW>::NW - 1; q >= 0; --q) {
+      kc.wave_w[q] = q < wave ? pw : 0.0f;
+      if (q < wave) pw *= aw;
+    }
+  }
   // Lion constants of this thread's (k, lane) slot, loaded once (the threads
   // tid < KP * LW apply Lion after every chunk).
   float lion_lr = 0.0f, lion_decay = 0.0f, lion_ss = 0.0f;
@@ -228,7 +258,7 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
       const Rsrc orr = rows_from(ob0, p.o_ss, 4, t_blk);
       const Rsrc zr = rows_from(zb0, p.z_save ? p.z_ss : p.o_ss, p.z_save ? 2 : 4, t_blk);
 
-      float u[R + 1], w[R];
+      float u[R + 1], w[R], zs[R];
       float A = 1.0f, Bv = 0.0f;
       // A block whose runs are all inside the chunk skips the per-token
       // checks (each loop below comes in both versions; the choice is the
@@ -289,10 +319,19 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
             Bv = __builtin_fmaf(mu, Bv, w[r]);
             A *= mu;
           }
-          if (p.z_save && (FULL || r < n_valid)) {
-            const float zz[1] = {z};
-            BufVec<__bf16, 1>::store(zr, lane_ok ? (uint32_t)(g * R) * z_row + (uint32_t)(d * 2) : kOffOOB,
-                                     (uint32_t)r * z_row, zz);
+          zs[r] = z;
+        }
+        // z for the backward after the loop (a branch per token would cut the
+        // run into one basic block per token)
+        if (p.z_save) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            if (FULL || r < n_valid) {
+              // default cache policy, as for out
+              __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (__bf16)zs[r]), zr,
+                                                    lane_ok ? (uint32_t)(g * R) * z_row + (uint32_t)(d * 2) : kOffOOB,
+                                                    (uint32_t)r * z_row, 0);
+            }
           }
         }
       };
@@ -302,28 +341,50 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
         pass1(std::false_type{});
       // Compose the runs: inclusive scan inside the wave (later map applied
       // after earlier: A = A_l A_e, B = A_l B_e + B_l), then the waves.
-      float iA = A, iB = Bv;
+      float s;
+      if (full) {
+        // Every run of a full block decays by ar = mu^R and every wave by aw =
+        // mu^(R GPW): the scan carries B alone with constant factors, and the
+        // state before wave q is carry aw^q + sum_{p<q} aw^(q-1-p) B_p, the
+        // waves' B read together (every wave waits one LDS round trip, not q).
+        float iB = Bv;
 #pragma unroll
-      for (int o = 1; o < GPW; o <<= 1) {
-        const float pA = __shfl_up(iA, o * LW, 64), pB = __shfl_up(iB, o * LW, 64);
-        if (gw >= o) {
-          iB = __builtin_fmaf(iA, pB, iB);
-          iA *= pA;
+        for (int o = 1, j = 0; o < GPW; o <<= 1, ++j) {
+          const float pB = __shfl_up(iB, o * LW, 64);
+          if (gw >= o) iB = __builtin_fmaf(kc.run_pow[j], pB, iB);
         }
+        float eB = __shfl_up(iB, LW, 64);
+        if (gw == 0) eB = 0.0f;
+        if (gw == GPW - 1) L.wB[wave][l] = iB;
+        __syncthreads();
+        float sw = L.carry[l] * kc.wave_pow;
+#pragma unroll
+        for (int q = 0; q < V10Lds<LW>::NW; ++q) sw = __builtin_fmaf(kc.wave_w[q], L.wB[q][l], sw);
+        s = __builtin_fmaf(kc.run_lead, sw, eB);
+      } else {
+        float iA = A, iB = Bv;
+#pragma unroll
+        for (int o = 1; o < GPW; o <<= 1) {
+          const float pA = __shfl_up(iA, o * LW, 64), pB = __shfl_up(iB, o * LW, 64);
+          if (gw >= o) {
+            iB = __builtin_fmaf(iA, pB, iB);
+            iA *= pA;
+          }
+        }
+        float eA = __shfl_up(iA, LW, 64), eB = __shfl_up(iB, LW, 64);
+        if (gw == 0) {
+          eA = 1.0f;
+          eB = 0.0f;
+        }
+        if (gw == GPW - 1) {
+          L.wA[wave][l] = iA;
+          L.wB[wave][l] = iB;
+        }
+        __syncthreads();
+        s = L.carry[l];
+        for (int q = 0; q < wave; ++q) s = __builtin_fmaf(L.wA[q][l], s, L.wB[q][l]);
+        s = __builtin_fmaf(eA, s, eB);
       }
-      float eA = __shfl_up(iA, LW, 64), eB = __shfl_up(iB, LW, 64);
-      if (gw == 0) {
-        eA = 1.0f;
-        eB = 0.0f;
-      }
-      if (gw == GPW - 1) {
-        L.wA[wave][l] = iA;
-        L.wB[wave][l] = iB;
-      }
-      __syncthreads();
-      float s = L.carry[l];
-      for (int q = 0; q < wave; ++q) s = __builtin_fmaf(L.wA[q][l], s, L.wB[q][l]);
-      s = __builtin_fmaf(eA, s, eB);
       // Replay, store bf16(s), proxy gradient.
       const uint32_t ovo = lane_ok ? (uint32_t)(g * R) * o_row + (uint32_t)(d * 4) : kOffOOB;
       auto replay = [&](auto full_c) {
@@ -334,7 +395,11 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
             s = __builtin_fmaf(mu, s, w[r]);
             const float so = __builtin_amdgcn_fmed3f(s, -1.0f, 1.0f);
             const float ov[1] = {(float)(__bf16)so};
-            BufVec<float, 1>::store(orr, ovo, (uint32_t)r * o_row, ov);
+            // default cache policy: the 32-byte pieces that the workgroups of
+            // one XCD store into a 128-byte line merge in its L2 before they
+            // are written (non-temporal stores reached HBM as partial lines:
+            // 1.84x the output bytes)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ov[0]), orr, ovo, (uint32_t)r * o_row, 0);
             if ((FULL && r + 1 < R) || r0 + r + 1 < len) {
               const float err = u[r + 1] - so;
               const float gv = err * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-3.0f * kLog2e * __builtin_fabsf(err)));
