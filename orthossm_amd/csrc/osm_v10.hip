@@ -438,10 +438,15 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
 
     // Reduce the proxy gradient over the runs (a fixed butterfly inside each
     // wave, then the waves in order), then Lion.
+    // All KP sums first, then one guarded block of stores: a guard per sum
+    // splits them into separate basic blocks and exposes the latency of
+    // each butterfly's cross-lane moves.
+    float gsum[KP];
 #pragma unroll
-    for (int k = 0; k < KP; ++k) {
-      const float v = sum_runs<LW>(gc[k]);
-      if (gw == 0) L.ws[wave][k][l] = v;
+    for (int k = 0; k < KP; ++k) gsum[k] = sum_runs<LW>(gc[k]);
+    if (gw == 0) {
+#pragma unroll
+      for (int k = 0; k < KP; ++k) L.ws[wave][k][l] = gsum[k];
     }
     __syncthreads();
     if (tid < KP * LW) {
