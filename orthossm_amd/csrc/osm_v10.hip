@@ -62,24 +62,80 @@ __device__ __forceinline__ void v10_softsign(float xb, float& absu, float& sgn) 
   sgn = xs >= 0.0f ? 1.0f : -1.0f;
 }
 
-// Sum over the runs of a wave (lanes l, l + LW, l + 2 LW, ...) in every
-// lane, as the butterfly v += v[lane ^ o] for o = LW, 2 LW, .. 32, with
-// cross-lane moves that stay in the VALU: a DPP row rotate by 8 (lane ^ 8
-// inside each 16-lane row) and the gfx950 row swaps, whose two results for
-// (v, v) are (row 0, row 0, row 2, row 2) and (row 1, row 1, row 3, row 3)
-// (v_permlane16_swap) and (lower half twice) and (upper half twice)
-// (v_permlane32_swap).  Each step adds a lane's value and its partner's, as
-// the butterfly does (the same sums, in either operand order).
-template <int LW>
-__device__ __forceinline__ float sum_runs(float v) {
+// The KP proxy-gradient sums of a wave's runs, reduce-scattered: the sum of
+// v over the runs of lane l (lanes l, l + LW, l + 2 LW, .. of the wave) is
+// the butterfly v += v[lane ^ o] for o = LW, 2 LW, .. 32, and here each step
+// serves two of the sums at once, so that after the last step lane (run gw,
+// l) holds the full sum of coefficient gw (and, with LW = 16 and KP = 8,
+// of gw + 4), which it stores to ws[k][l].  The steps, with the same sums
+// (each adds a lane's partial sum and its partner's) as the butterfly:
+//   o = 8 (LW = 8): a DPP row rotate by 8 (lane ^ 8 inside each 16-lane row)
+//     of the value the partner keeps (lanes with bit 3 set keep the odd one
+//     of a pair of sums, the others the even one);
+//   o = 16: v_permlane16_swap of a pair (a, b) gives (rows a0, b0, a2, b2)
+//     and (rows a1, b1, a3, b3): their sum holds a's pair sums in the even
+//     rows and b's in the odd rows;
+//   o = 32: v_permlane32_swap of (a, b) gives (lower a, lower b) and (upper
+//     a, upper b): their sum holds a's sums in the lower half and b's in the
+//     upper half.
+// (Lane layout of the two swaps, for equal operands, checked by a probe
+// kernel: rows 0, 0, 2, 2 and 1, 1, 3, 3; lower half twice and upper half
+// twice.)  With KP = 4 the last step has one value and adds the halves as
+// the butterfly does.
+__device__ __forceinline__ void swap16(float& a, float& b) {
   typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+  const u32x2v r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r.x);
+  b = __uint_as_float(r.y);
+}
+__device__ __forceinline__ void swap32(float& a, float& b) {
+  typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+  const u32x2v r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r.x);
+  b = __uint_as_float(r.y);
+}
+// pair sum for o = 16 / 32: a + b after the swap
+__device__ __forceinline__ float pair16(float a, float b) {
+  swap16(a, b);
+  return a + b;
+}
+__device__ __forceinline__ float pair32(float a, float b) {
+  swap32(a, b);
+  return a + b;
+}
+
+template <int LW, int KP>
+__device__ __forceinline__ void store_run_sums(const float (&gc)[KP], float (&ws)[8][LW], int l, int gw) {
   static_assert(LW == 8 || LW == 16, "8 or 16 lanes per workgroup");
-  if constexpr (LW == 8)
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
-  const u32x2v a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(a.x) + __uint_as_float(a.y);
-  const u32x2v b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(b.x) + __uint_as_float(b.y);
+  static_assert(KP == 4 || KP == 8, "4 or 8 coefficients");
+  constexpr int N1 = LW == 8 ? KP / 2 : KP;   // values left after the o = 8 step
+  float a[N1];
+  if constexpr (LW == 8) {
+    const bool odd = (threadIdx.x & 8) != 0;
+#pragma unroll
+    for (int i = 0; i < N1; ++i) {
+      const float keep = odd ? gc[2 * i + 1] : gc[2 * i];
+      const float give = odd ? gc[2 * i] : gc[2 * i + 1];
+      a[i] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(give), 0x128, 0xF, 0xF, false));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N1; ++i) a[i] = gc[i];
+  }
+  constexpr int N2 = N1 / 2;   // after o = 16
+  float b[N2];
+#pragma unroll
+  for (int i = 0; i < N2; ++i) b[i] = pair16(a[2 * i], a[2 * i + 1]);
+  if constexpr (N2 == 1) {
+    // one value (LW = 8, KP = 4): lane (gw, l) holds coefficient gw & 3
+    const float v = pair32(b[0], b[0]);
+    if (gw < 4) ws[gw][l] = v;
+  } else {
+    // N2 = 2 (LW = 8, KP = 8: coefficient gw) or N2 = 4 (LW = 16, KP = 8:
+    // coefficients gw and gw + 4) or N2 = 2 (LW = 16, KP = 4: gw)
+#pragma unroll
+    for (int i = 0; i < N2 / 2; ++i) ws[gw + 4 * i][l] = pair32(b[2 * i], b[2 * i + 1]);
+  }
 }
 
 // 16-byte aligned: LUT rows are read as f32x4.
@@ -437,17 +493,9 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
     }
 
     // Reduce the proxy gradient over the runs (a fixed butterfly inside each
-    // wave, then the waves in order), then Lion.
-    // All KP sums first, then one guarded block of stores: a guard per sum
-    // splits them into separate basic blocks and exposes the latency of
-    // each butterfly's cross-lane moves.
-    float gsum[KP];
-#pragma unroll
-    for (int k = 0; k < KP; ++k) gsum[k] = sum_runs<LW>(gc[k]);
-    if (gw == 0) {
-#pragma unroll
-      for (int k = 0; k < KP; ++k) L.ws[wave][k][l] = gsum[k];
-    }
+    // wave, reduce-scattered over the coefficients, then the waves in
+    // order), then Lion.
+    store_run_sums<LW, KP>(gc, L.ws[wave], l, gw);
     __syncthreads();
     if (tid < KP * LW) {
       const int k = tid / LW, ll = tid % LW;
