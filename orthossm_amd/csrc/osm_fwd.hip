@@ -141,28 +141,20 @@ cheby_ema_fwd_kernel(const FwdParams p) {
   __shared__ float mono[KP][G::LANES];
   const auto ml = mono_issue<KP, G>(p, q, ti, a);
 
-  // x rows of this thread's run, g (dynamic lambda).
-  float w[R][LPT];
-  {
-    uint32_t so = 0;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      BufVec<XT, LPT>::load(a.x, a.vx, so, w[r]);
-      so = next_off(so, a.sx);
-    }
-  }
   const float lam_h = p.lam[a.h];
   // Dynamic lambda: the workgroup loads g for the tile's tokens and the
   // heads its lanes span (one value per token and head, not one per thread)
   // and forms lambda = clamp(lam_h + lam_shift g) once into LDS,
   // lam_s[head - h0][token]; threads read their run's row from there in
-  // both passes instead of holding R values in registers.
+  // both passes instead of holding R values in registers.  g and lam_h are
+  // loaded before x: forming lambda waits for them, and loads complete in
+  // order, so with x issued first that wait was a wait for all of x.
   constexpr int NHB = DYN ? (LPT == 1 ? G::LANES : G::LANES / 4) : 1;   // heads a lane-block can span
   constexpr int kGL = 2;   // g loads per thread held in registers (the rest: a rare loop)
   static_assert(!DYN || (R % 4 == 0 && G::TILE % 4 == 0), "runs read lambda four tokens at a time");
   __shared__ __attribute__((aligned(16))) float lam_s[NHB][DYN ? G::TILE : 1];
   int h0 = 0, n_gl = 0;
-  float glv[kGL];
+  float glv[kGL], lhv[kGL];
   if constexpr (DYN) {
     const int d0 = ti.lbd * G::LANES;
     h0 = div_hd(d0, p);
@@ -174,25 +166,36 @@ cheby_ema_fwd_kernel(const FwdParams p) {
       float v[1];
       BufVec<float, 1>::load(a.g, idx < n_gl ? (uint32_t)((t * p.g_ss + (h0 + hh) * p.g_sh) * 4) : kOffOOB, 0, v);
       glv[i] = v[0];
+      lhv[i] = p.lam[min(h0 + hh, p.H - 1)];   // (idx >= n_gl: not used)
     }
   }
 
+  // x rows of this thread's run.
+  float w[R][LPT];
+  {
+    uint32_t so = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      BufVec<XT, LPT>::load(a.x, a.vx, so, w[r]);
+      so = next_off(so, a.sx);
+    }
+  }
   __builtin_amdgcn_s_setprio(0);
   __shared__ unsigned mono_big[KP * G::NSUB];
   mono_store<KP, G>(ml, q, mono, mono_big);
   if constexpr (DYN) {
-    auto lam_of = [&](int idx, float gv) {
+    auto lam_of = [&](int idx, float gv, float lh) {
       const int t = idx % G::TILE, hh = idx / G::TILE;
-      lam_s[hh][t] = __builtin_amdgcn_fmed3f(__builtin_fmaf(p.lam_shift, gv, p.lam[h0 + hh]), p.lam_min, p.lam_max);
+      lam_s[hh][t] = __builtin_amdgcn_fmed3f(__builtin_fmaf(p.lam_shift, gv, lh), p.lam_min, p.lam_max);
     };
 #pragma unroll
     for (int i = 0; i < kGL; ++i)
-      if (q.tid + i * G::THREADS < n_gl) lam_of(q.tid + i * G::THREADS, glv[i]);
+      if (q.tid + i * G::THREADS < n_gl) lam_of(q.tid + i * G::THREADS, glv[i], lhv[i]);
     for (int idx = q.tid + kGL * G::THREADS; idx < n_gl; idx += G::THREADS) {   // small heads only
       float v[1];
       const int t = idx % G::TILE, hh = idx / G::TILE;
       BufVec<float, 1>::load(a.g, (uint32_t)((t * p.g_ss + (h0 + hh) * p.g_sh) * 4), 0, v);
-      lam_of(idx, v[0]);
+      lam_of(idx, v[0], p.lam[h0 + hh]);
     }
   }
   __syncthreads();
