@@ -18,12 +18,15 @@
  *
  * Reference interfaces replaced (paths relative to the OrthoSSM root):
  *   osm_cheby_ema_fwd  the forward kernel launches
- *                      _launch_ortho_megakernel (sdpc_kernel.py:2290-2344),
- *                      the _EMAFastPathFn launch (sdpc_kernel.py:1661-1670) and
- *                      the direct _fused_clenshaw_ema_kernel launch in
- *                      precision_tests.py:47-73, with the EMA carry
- *                      InitState/FinalState [B,D] (sdpc_kernel.py:1999-2003,
- *                      2172-2177) exposed as ema_init / ema_final.
+ *                      _launch_ortho_megakernel (sdpc_kernel.py:2290-2344) and
+ *                      the _EMAFastPathFn launch (sdpc_kernel.py:1661-1670),
+ *                      with the EMA carry InitState/FinalState [B,D]
+ *                      (sdpc_kernel.py:1999-2003, 2172-2177) exposed as
+ *                      ema_init / ema_final.
+ *   osm_cheby_ema_lut_fwd  the direct _fused_clenshaw_ema_kernel launch
+ *                      (sdpc_kernel.py:988-1209; precision_tests.py:47-73):
+ *                      LUT or Clenshaw series, x_norm, tanh_y, clamped EMA
+ *                      from InitState, FinalState.
  *   osm_cheby_ema_ttt  the coefficient-gradient chain of FusedChebyRKVv10.backward:
  *                      _parallel_reverse_ema_kernel (sdpc_kernel.py:2463-2471),
  *                      _parallel_backward_clenshaw_kernel_v10 (2487-2500) and
@@ -241,6 +244,45 @@ typedef struct osm_v10_args {
                                    has to reach the host */
 } osm_v10_args;
 
+/*
+ * Fixed-coefficient fused forward of the same kernel family: the reference's
+ * _fused_clenshaw_ema_kernel (sdpc_kernel.py:988-1209), which
+ * precision_tests.py:33-73 launches.  Per lane, over all S tokens:
+ *
+ *   x_norm = sign(x)(1 - 1/(1 + max(|x|, 1e-7)))   on x as given; NaN reads as 0
+ *   y = LUT(x_norm) (OSM_V10_USE_LUT, as osm_v10_args) or Clenshaw over c0..c3
+ *       (K <= 4) or c0..c7 (K > 4)
+ *   tanh_y = tanh(clamp((0.98 - 0.06 h/H) y, -4, 4))   (0 for NaN x)
+ *   s = mu s + (1 - mu) tanh_y from s = ema_init;  out = clamp(s, -1, 1) (fp32)
+ *
+ * with the carried state clamped to [-1, 1] at every clamp_tile-th token
+ * (the kernel's BLOCK_S tile carry), and ema_final = clamp of the state after
+ * token S-1.  One launch, no workspace.
+ */
+typedef struct osm_lut_fwd_args {
+  int32_t abi_version;          /* = OSM_ABI_VERSION */
+  int32_t flags;                /* OSM_V10_USE_LUT */
+  int64_t B, S, H, hd, K;       /* 1 <= K <= 8 */
+  int64_t clamp_tile;           /* >= 16, a multiple of 16 */
+  const void* x;                /* [B,S,H*hd], x_dtype; lane stride 1 */
+  int32_t x_dtype;
+  int64_t x_stride_b, x_stride_s;
+  const float* coeffs;          /* [B,H,K,hd] fp32, lane stride 1 */
+  int64_t c_stride_b, c_stride_h, c_stride_k;
+  const float* lut;             /* [8,256] fp32 contiguous (with OSM_V10_USE_LUT) */
+  float ema_momentum;
+  const float* ema_init;        /* optional [B, H*hd] fp32, lane stride 1 (NULL: 0) */
+  int64_t init_stride_b;
+  float* out;                   /* [B,S,H*hd] fp32, lane stride 1 */
+  int64_t out_stride_b, out_stride_s;
+  float* x_norm;                /* optional [B,S,H*hd] fp32, lane stride 1 */
+  int64_t xn_stride_b, xn_stride_s;
+  float* tanh_y;                /* optional [B,S,H*hd] fp32, lane stride 1 */
+  int64_t ty_stride_b, ty_stride_s;
+  float* ema_final;             /* optional [B, H*hd] fp32, lane stride 1 */
+  int64_t final_stride_b;
+} osm_lut_fwd_args;
+
 /* Which entry point a workspace is sized for. */
 typedef enum osm_op { OSM_OP_FWD = 0, OSM_OP_TTT = 1, OSM_OP_BWD = 2 } osm_op;
 
@@ -301,6 +343,11 @@ int osm_cheby_ema_ttt(const osm_cheby_args* args, float* grad, int target, void*
 /* The full-path chunk loop described above osm_v10_args, in one launch on
  * `stream`.  Needs no workspace. */
 int osm_v10_chunked_ttt(const osm_v10_args* args, void* stream);
+
+/* The fixed-coefficient forward described above osm_lut_fwd_args, in one
+ * launch on `stream` (replaces a launch of _fused_clenshaw_ema_kernel,
+ * sdpc_kernel.py:988-1209).  Needs no workspace. */
+int osm_cheby_ema_lut_fwd(const osm_lut_fwd_args* args, void* stream);
 
 /* Backward of osm_cheby_ema_fwd: writes grad_x and, when non-NULL,
  * grad_coeffs and grad_init.  Replaces the backward listed in the header

@@ -216,6 +216,64 @@ def v10_full(x, coeffs, momentum, *, n_heads=4, base_lr=0.005, ema_momentum=0.9,
     return np.concatenate(outs, axis=1), c, m
 
 
+def clenshaw8_series(c, u):
+    """The fused Clenshaw + EMA kernel's Clenshaw above four coefficients
+    (sdpc_kernel.py:1148-1156): all of c0..c7 enter (zeros past K),
+    b_k = 2u b_{k+1} - b_{k+2} + c_k, y = u b_1 - b_2 + c_0."""
+    K = c.shape[-1]
+    ck = [c[..., k] if k < K else 0.0 for k in range(8)]
+    b1, b2 = ck[7], 0.0
+    for k in range(6, 0, -1):
+        b1, b2 = 2.0 * u * b1 - b2 + ck[k], b1
+    return u * b1 - b2 + ck[0]
+
+
+def fused_clenshaw_ema(x, coeffs, *, n_heads, ema_momentum=0.9, ema_init=None, use_lut=True, lut=None,
+                       block_s=128):
+    """The reference's _fused_clenshaw_ema_kernel (sdpc_kernel.py:988-1209)
+    in float64: x as given (no bf16 rounding; callers pass bf16 x when they
+    want it), the megakernel's softsign (1079-1085), the LUT series
+    (1101-1141) or Clenshaw over c0..c3 for K <= 4 and c0..c7 above
+    (1142-1156), damping 0.98 - 0.06 h/H and the clamped exp-form tanh with
+    NaN x -> 0 (1158-1165), then per tile of ``block_s`` tokens the EMA from
+    the carried state, out = clamp(s, -1, 1), and the carry into the next
+    tile = out at the tile's last token (1176-1200); the final state is the
+    last carry (1206-1209; ema_init itself when S = 0).
+
+    x [B,S,D], coeffs [B,H,K,hd] (K <= 8), ema_init [B,D] or None;
+    ema_momentum is used as given (the kernel receives it as a float32
+    argument, so parity checks pass that value).  Returns (x_norm, tanh_y,
+    out, final) as float64."""
+    x = np.asarray(x, dtype=np.float64)
+    B, S, D = x.shape
+    c = np.asarray(coeffs, dtype=np.float64)
+    H = n_heads
+    _, _, K, hd = c.shape
+    assert c.shape[1] == H and H * hd == D and 1 <= K <= MAX_DEGREE
+    u, absu, sign, nan = v10_softsign(x)
+    cl = c.transpose(0, 1, 3, 2).reshape(B, 1, D, K)
+    if use_lut:
+        y = lut_series(cl, absu, sign, lut if lut is not None else chebyshev_lut())
+    elif K <= 4:
+        y = clenshaw4_series(cl, u)
+    else:
+        y = clenshaw8_series(cl, u)
+    gamma = np.repeat(0.98 - 0.06 * np.arange(H) / H, hd)
+    yc = np.clip(y * gamma, -4.0, 4.0)
+    e2 = np.exp(2.0 * yc)
+    z = np.where(nan, 0.0, (e2 - 1.0) / (e2 + 1.0))
+    mu = float(ema_momentum)
+    carry = np.zeros((B, D)) if ema_init is None else np.asarray(ema_init, np.float64).reshape(B, D).copy()
+    out = np.empty((B, S, D))
+    for t0 in range(0, S, block_s):
+        state = carry
+        for t in range(t0, min(t0 + block_s, S)):
+            state = mu * state + (1.0 - mu) * z[:, t]
+            out[:, t] = np.clip(state, -1.0, 1.0)
+        carry = out[:, min(t0 + block_s, S) - 1]
+    return u, z, out, carry
+
+
 def v10_backward(x, out, zb, hist, grad_out, *, n_heads, ema_momentum, chunk):
     """The reference's backward of the full path (FusedChebyRKVv10.backward,
     sdpc_kernel.py:2436-2515) applied to every chunk (the chunk loop,

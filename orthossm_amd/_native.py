@@ -56,6 +56,7 @@ EXPORTS = (
     "osm_cheby_ema_ttt",
     "osm_cheby_ema_bwd",
     "osm_v10_chunked_ttt",
+    "osm_cheby_ema_lut_fwd",
 )
 
 
@@ -163,6 +164,44 @@ class V10Args(ctypes.Structure):
     ]
 
 
+class LutFwdArgs(ctypes.Structure):
+    """Mirror of ``osm_lut_fwd_args``."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+        ("B", ctypes.c_int64),
+        ("S", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("hd", ctypes.c_int64),
+        ("K", ctypes.c_int64),
+        ("clamp_tile", ctypes.c_int64),
+        ("x", ctypes.c_void_p),
+        ("x_dtype", ctypes.c_int32),
+        ("x_stride_b", ctypes.c_int64),
+        ("x_stride_s", ctypes.c_int64),
+        ("coeffs", ctypes.c_void_p),
+        ("c_stride_b", ctypes.c_int64),
+        ("c_stride_h", ctypes.c_int64),
+        ("c_stride_k", ctypes.c_int64),
+        ("lut", ctypes.c_void_p),
+        ("ema_momentum", ctypes.c_float),
+        ("ema_init", ctypes.c_void_p),
+        ("init_stride_b", ctypes.c_int64),
+        ("out", ctypes.c_void_p),
+        ("out_stride_b", ctypes.c_int64),
+        ("out_stride_s", ctypes.c_int64),
+        ("x_norm", ctypes.c_void_p),
+        ("xn_stride_b", ctypes.c_int64),
+        ("xn_stride_s", ctypes.c_int64),
+        ("tanh_y", ctypes.c_void_p),
+        ("ty_stride_b", ctypes.c_int64),
+        ("ty_stride_s", ctypes.c_int64),
+        ("ema_final", ctypes.c_void_p),
+        ("final_stride_b", ctypes.c_int64),
+    ]
+
+
 class OsmError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"{STATUS.get(code, code)}: {msg}")
@@ -209,6 +248,8 @@ def load() -> ctypes.CDLL:
                                           ctypes.c_size_t, ctypes.c_void_p]
         lib.osm_v10_chunked_ttt.restype = ctypes.c_int
         lib.osm_v10_chunked_ttt.argtypes = [ctypes.POINTER(V10Args), ctypes.c_void_p]
+        lib.osm_cheby_ema_lut_fwd.restype = ctypes.c_int
+        lib.osm_cheby_ema_lut_fwd.argtypes = [ctypes.POINTER(LutFwdArgs), ctypes.c_void_p]
         got = lib.osm_abi_version()
         if got != ABI_VERSION:
             raise ImportError(f"orthossm_amd: library ABI {got} != binding ABI {ABI_VERSION}; rebuild")

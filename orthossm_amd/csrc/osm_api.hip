@@ -525,6 +525,96 @@ int osm_v10_chunked_ttt(const osm_v10_args* a, void* stream) {
   return ok();
 }
 
+int osm_cheby_ema_lut_fwd(const osm_lut_fwd_args* a, void* stream) {
+  if (!a) return fail(OSM_E_ARG, "args is NULL");
+  if (a->abi_version != OSM_ABI_VERSION)
+    return fail(OSM_E_ARG, "abi_version %d does not match library ABI %d", a->abi_version, OSM_ABI_VERSION);
+  if (a->flags & ~OSM_V10_USE_LUT) return fail(OSM_E_ARG, "unknown flag bits 0x%x", a->flags);
+  if (a->B < 0 || a->S < 0 || a->H < 1 || a->hd < 1)
+    return fail(OSM_E_SHAPE, "need B, S >= 0, H, hd >= 1 (B=%lld S=%lld H=%lld hd=%lld)", (long long)a->B,
+                (long long)a->S, (long long)a->H, (long long)a->hd);
+  // The reference kernel loads eight coefficients at most (sdpc_kernel.py:1047-1054).
+  if (a->K < 1 || a->K > 8) return fail(OSM_E_SHAPE, "K=%lld outside [1, 8]", (long long)a->K);
+  // The carried state is clamped between waves of 16 or 32 tokens.
+  if (a->clamp_tile < 16 || a->clamp_tile % 16 || a->clamp_tile >= (int64_t(1) << 30))
+    return fail(OSM_E_SHAPE, "clamp_tile=%lld must be a multiple of 16", (long long)a->clamp_tile);
+  if (a->x_dtype != OSM_F32 && a->x_dtype != OSM_BF16) return fail(OSM_E_DTYPE, "x_dtype %d unsupported", a->x_dtype);
+  const int64_t D = a->H * a->hd;
+  if (D > (int64_t(1) << 28) || a->S >= (int64_t(1) << 31)) return fail(OSM_E_SHAPE, "problem too large");
+  if (a->B == 0) return ok();
+  // (S = 0 reads and writes no rows: only ema_final, from ema_init)
+  if (a->S > 0 && (!a->x || !a->coeffs || !a->out || ((a->flags & OSM_V10_USE_LUT) && !a->lut)))
+    return fail(OSM_E_ARG, "x, coeffs, out (and lut with OSM_V10_USE_LUT) must be non-NULL");
+  const int xs = a->x_dtype == OSM_F32 ? 4 : 2;
+  if ((uintptr_t)a->x % xs || a->x_stride_b < 0 || a->x_stride_s < 0)
+    return fail(OSM_E_LAYOUT, "x must be element-aligned with non-negative strides");
+  // Row outputs: aligned, rows and batches not overlapping.
+  struct RowOut {
+    const float* p;
+    int64_t sb, ss;
+    const char* what;
+  };
+  const RowOut outs[3] = {{a->out, a->out_stride_b, a->out_stride_s, "out"},
+                          {a->x_norm, a->xn_stride_b, a->xn_stride_s, "x_norm"},
+                          {a->tanh_y, a->ty_stride_b, a->ty_stride_s, "tanh_y"}};
+  const int64_t lim = int64_t(1) << 31;
+  const int64_t blk_rows = osm::kV10Groups * osm::kV10Run + 1;
+  for (const RowOut& o : outs) {
+    if (!o.p) continue;
+    if ((uintptr_t)o.p % 4 || o.ss < D || o.sb < a->S * o.ss)
+      return fail(OSM_E_LAYOUT, "%s misaligned or its rows/batches overlap", o.what);
+    if ((blk_rows * o.ss + D) * 4 >= lim) return fail(OSM_E_LAYOUT, "%s token stride too large", o.what);
+  }
+  if ((blk_rows * a->x_stride_s + D) * xs >= lim)
+    return fail(OSM_E_LAYOUT, "token stride too large: 257 rows span more than 2 GiB");
+  if (a->c_stride_b < 0 || a->c_stride_h < 0 || a->c_stride_k < 0)
+    return fail(OSM_E_LAYOUT, "coeffs strides must be non-negative");
+  if (a->ema_init && ((uintptr_t)a->ema_init % 4 || a->init_stride_b < 0))
+    return fail(OSM_E_LAYOUT, "ema_init misaligned or with a negative stride");
+  if (a->ema_final && ((uintptr_t)a->ema_final % 4 || a->final_stride_b < D))
+    return fail(OSM_E_LAYOUT, "ema_final misaligned or its rows overlap");
+  osm::V10FixedParams p{};
+  p.x = a->x;
+  p.out = a->out;
+  p.coeffs = a->coeffs;
+  p.lut = a->lut;
+  p.x_sb = a->x_stride_b;
+  p.x_ss = a->x_stride_s;
+  p.o_sb = a->out_stride_b;
+  p.o_ss = a->out_stride_s;
+  p.c_sb = a->c_stride_b;
+  p.c_sh = a->c_stride_h;
+  p.c_sk = a->c_stride_k;
+  p.B = (int)a->B;
+  p.S = (int)a->S;
+  p.H = (int)a->H;
+  p.hd = (int)a->hd;
+  p.K = (int)a->K;
+  p.D = (int)D;
+  p.chunk = (int)std::max<int64_t>(a->S, 1);   // one chunk; none when S = 0
+  // Waves of 32 tokens with 8 lanes per workgroup, 16 with 16 lanes: the
+  // clamp boundaries fall between waves.
+  p.lanes = a->clamp_tile % 32 ? 16 : osm::v10_lanes(a->B, a->H, a->hd);
+  p.n_lg = (int)((a->hd + p.lanes - 1) / p.lanes);
+  p.mu = a->ema_momentum;
+  p.ema_init = a->ema_init;
+  p.init_sb = a->init_stride_b;
+  p.ema_final = a->ema_final;
+  p.final_sb = a->final_stride_b;
+  p.xnorm = a->x_norm;
+  p.xn_sb = a->xn_stride_b;
+  p.xn_ss = a->xn_stride_s;
+  p.tanhy = a->tanh_y;
+  p.ty_sb = a->ty_stride_b;
+  p.ty_ss = a->ty_stride_s;
+  p.clamp_tile = (int)a->clamp_tile;
+  if ((int64_t)p.B * p.H * p.n_lg >= (int64_t(1) << 31)) return fail(OSM_E_SHAPE, "problem too large");
+  const hipError_t e = osm::launch_v10_fixed(p, a->x_dtype, (a->flags & OSM_V10_USE_LUT) != 0, a->K <= 4 ? 4 : 8,
+                                             static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "fixed-coefficient forward launch");
+  return ok();
+}
+
 int osm_cheby_ema_bwd(const osm_cheby_args* args, const osm_cheby_bwd_args* bwd, void* workspace,
                       size_t workspace_bytes, void* stream) {
   Geometry geo;

@@ -207,6 +207,20 @@ struct V10Params {
   float mu, base_lr, beta1, beta2, wd;
 };
 
+// The fixed-coefficient forward (osm_cheby_ema_lut_fwd) on the same kernel:
+// one chunk of S tokens, no Lion, x as given, EMA from ema_init, out =
+// clamp(s) in fp32, the carried state clamped every clamp_tile tokens, and
+// optional x_norm, tanh_y and ema_final outputs.  (A separate struct, so the
+// full path's kernel arguments stay as they are.)
+struct V10FixedParams : V10Params {
+  const float* ema_init;       // [B, D] (row stride init_sb) or NULL (0)
+  float* ema_final;            // [B, D] (row stride final_sb) or NULL
+  float* xnorm;                // [B,S,D] fp32 or NULL
+  float* tanhy;                // [B,S,D] fp32 or NULL
+  int64_t init_sb, final_sb, xn_sb, xn_ss, ty_sb, ty_ss;
+  int clamp_tile;              // tokens between clamps of the carried state
+};
+
 // Multiplier and shift that divide by v (1 <= v < 2^31) for dividends
 // 0 <= n < 2^31: s = ceil(log2 v), m = floor(2^32 (2^s - v) / v) + 1
 // (Granlund and Montgomery, "Division by invariant integers using
@@ -233,6 +247,7 @@ hipError_t launch_ttt(const FwdParams& p, float* grad, int x_dtype, int out_dtyp
 hipError_t launch_bwd(const BwdParams& p, int x_dtype, int out_dtype, bool dyn, int tile, int kpad,
                       hipStream_t stream);
 hipError_t launch_v10(const V10Params& p, int x_dtype, bool use_lut, int kpad, hipStream_t stream);
+hipError_t launch_v10_fixed(const V10FixedParams& p, int x_dtype, bool use_lut, int kpad, hipStream_t stream);
 hipError_t launch_fill_zero(void* ptr, size_t bytes, hipStream_t stream);
 hipError_t launch_copy_state(const float* src, float* dst, size_t n, hipStream_t stream);
 hipError_t launch_ws_status(void* ws, unsigned* dst, int reset, hipStream_t stream);

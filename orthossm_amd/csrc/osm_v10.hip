@@ -154,8 +154,18 @@ struct __attribute__((aligned(16))) V10Lds {
 // 256-token block.  A wave holds 64 / LW runs of the same LW lanes: runs are
 // composed inside a wave with shuffles and across waves through LDS, both
 // in a fixed order.
-template <typename XT, int KP, bool LUT, int LW>
-__global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10Params p) {
+//
+// FIXED: the fixed-coefficient forward of _fused_clenshaw_ema_kernel
+// (sdpc_kernel.py:988-1209) on the same machinery: one chunk of S tokens, x
+// as given (no bf16 rounding), the 8-term Clenshaw fallback above four
+// coefficients (1148-1156; the megakernel's fallback stops at four,
+// 2070-2077), the EMA from ema_init with the carried state clamped to
+// [-1, 1] at every clamp_tile-th token boundary (the kernel's tile carry,
+// 1193-1200), out = clamp(s) in fp32, x_norm and tanh_y stored, the state
+// after token S-1 to ema_final; no proxy gradient and no Lion.
+template <typename XT, int KP, bool LUT, int LW, bool FIXED, typename P>
+__global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const P p) {
+  static_assert(FIXED == std::is_same<P, V10FixedParams>::value, "fixed forward, fixed parameters");
   constexpr int kThreads = kV10Groups * LW;
   constexpr int GPW = 64 / LW;        // runs per wave
   constexpr int R = kV10Run;
@@ -186,15 +196,18 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
   const bool lane_ok = j < p.hd;
   const int d = h * p.hd + j;
 
-  // Tables and the lanes' starting coefficients and momentum.
+  // Tables and the lanes' starting coefficients and momentum (the fixed
+  // forward with S = 0 has neither: it only passes ema_init through).
+  const bool rows = !FIXED || p.S > 0;
   if constexpr (LUT) {
-    for (int i = tid; i < 256 * 8; i += kThreads) L.lut[i % 256][i / 256] = p.lut[i];
+    if (rows)
+      for (int i = tid; i < 256 * 8; i += kThreads) L.lut[i % 256][i / 256] = p.lut[i];
   }
   if (tid < KP * LW) {
     const int k = tid / LW, ll = tid % LW, jj = lg * LW + ll;
-    const bool ok = jj < p.hd && k < p.K;
+    const bool ok = rows && jj < p.hd && k < p.K;
     L.cs[k][ll] = ok ? p.coeffs[(int64_t)b * p.c_sb + (int64_t)h * p.c_sh + (int64_t)k * p.c_sk + jj] : 0.0f;
-    L.ms[k][ll] = ok ? p.momentum[(int64_t)b * p.m_sb + (int64_t)h * p.m_sh + (int64_t)k * p.m_sk + jj] : 0.0f;
+    L.ms[k][ll] = ok && !FIXED ? p.momentum[(int64_t)b * p.m_sb + (int64_t)h * p.m_sh + (int64_t)k * p.m_sk + jj] : 0.0f;
   }
   const float gamma = 0.98f - 0.06f * (float)h / (float)p.H;
   const float mu = p.mu_dev ? *p.mu_dev : p.mu, one_m = 1.0f - mu;
@@ -231,7 +244,7 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
   // Lion constants of this thread's (k, lane) slot, loaded once (the threads
   // tid < KP * LW apply Lion after every chunk).
   float lion_lr = 0.0f, lion_decay = 0.0f, lion_ss = 0.0f;
-  if (tid < KP * LW) {
+  if (!FIXED && tid < KP * LW) {
     const int k = tid / LW;
     lion_lr = p.base_lr * p.lr_scale[h];
     float lam = p.lion_lambda[h];
@@ -255,6 +268,15 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
   const uint32_t x_row = (uint32_t)(p.x_ss * sizeof(XT));   // bytes per token
   const uint32_t o_row = (uint32_t)(p.o_ss * 4);
   const uint32_t z_row = (uint32_t)(p.z_ss * 2);
+  const char* xnb0 = ob0;
+  const char* tyb0 = ob0;
+  uint32_t xn_row = 0, ty_row = 0;
+  if constexpr (FIXED) {
+    if (p.xnorm) xnb0 = reinterpret_cast<const char*>(p.xnorm) + (int64_t)b * p.xn_sb * 4;
+    if (p.tanhy) tyb0 = reinterpret_cast<const char*>(p.tanhy) + (int64_t)b * p.ty_sb * 4;
+    xn_row = (uint32_t)(p.xn_ss * 4);
+    ty_row = (uint32_t)(p.ty_ss * 4);
+  }
   __syncthreads();
 
   // x rows of a run, double-buffered: the rows of the next block (or of the
@@ -277,7 +299,7 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
       so = next_off(so, x_row);
     }
   };
-  load_run(xcur, 0);
+  if (!FIXED || n_chunks > 0) load_run(xcur, 0);   // (the fixed forward takes S = 0: no rows)
   // Wait for these rows here, once.  Without it the compiler, merging this
   // path with the loop's back edge, waits for the next block's prefetched
   // rows at the start of every block (vmcnt 4..1 before each row's use),
@@ -298,7 +320,14 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
     float gc[KP];
 #pragma unroll
     for (int k = 0; k < KP; ++k) gc[k] = 0.0f;
-    if (tid < LW) L.carry[tid] = 0.0f;
+    if (tid < LW) {
+      float c0 = 0.0f;
+      if constexpr (FIXED) {
+        const int jj = lg * LW + tid;
+        if (p.ema_init && jj < p.hd) c0 = p.ema_init[(int64_t)b * p.init_sb + h * p.hd + jj];
+      }
+      L.carry[tid] = c0;
+    }
 
     for (int blk = 0; blk * kBlockTok < len; ++blk) {
       const int r0 = blk * kBlockTok + g * R;            // run start inside the chunk
@@ -320,12 +349,14 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
       // checks (each loop below comes in both versions; the choice is the
       // same for the whole workgroup): only the last token of a run may
       // lack its pair (the chunk's last token), checked once per run.
-      const bool full = (blk + 1) * kBlockTok <= len;
+      // (the fixed-coefficient forward takes the general path, whose wave
+      // composition clamps the carried state at tile boundaries)
+      const bool full = !FIXED && (blk + 1) * kBlockTok <= len;
       auto pass1 = [&](auto full_c) {
         constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
         for (int r = 0; r <= R; ++r) {
-          const float xb = to_bf16_value<XT>(xcur[r]);
+          const float xb = FIXED ? xcur[r] : to_bf16_value<XT>(xcur[r]);
           float absu, sgn;
           v10_softsign(xb, absu, sgn);
           u[r] = sgn * absu;
@@ -359,6 +390,19 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
             }
             const float ya = __builtin_fmaf(sgn, ao, ae), yb = __builtin_fmaf(sgn, bo, be);
             y = __builtin_fmaf(fr, yb - ya, ya);
+          } else if (FIXED && KP > 4) {
+            // Clenshaw over all eight terms, as _fused_clenshaw_ema_kernel
+            // above four coefficients: b_k = 2u b_{k+1} - b_{k+2} + c_k,
+            // y = u b_1 - b_2 + c_0 (zeros past K).
+            const float uu = u[r], u2 = uu + uu;
+            float bk1 = c[KP - 1], bk2 = 0.0f;
+#pragma unroll
+            for (int k = KP - 2; k >= 1; --k) {
+              const float bk = __builtin_fmaf(u2, bk1, c[k]) - bk2;
+              bk2 = bk1;
+              bk1 = bk;
+            }
+            y = __builtin_fmaf(uu, bk1, c[0]) - bk2;
           } else {
             const float uu = u[r], u2 = uu + uu;
             const float c3 = c[3], c2 = c[2];
@@ -387,6 +431,22 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
               __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (__bf16)zs[r]), zr,
                                                     lane_ok ? (uint32_t)(g * R) * z_row + (uint32_t)(d * 2) : kOffOOB,
                                                     (uint32_t)r * z_row, 0);
+            }
+          }
+        }
+        if constexpr (FIXED) {
+          // x_norm = u and tanh_y = z of the valid tokens, fp32
+          const uint32_t xo = lane_ok ? (uint32_t)(g * R) * xn_row + (uint32_t)(d * 4) : kOffOOB;
+          const uint32_t yo = lane_ok ? (uint32_t)(g * R) * ty_row + (uint32_t)(d * 4) : kOffOOB;
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            if (r < n_valid) {
+              if (p.xnorm)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(u[r]), rows_from(xnb0, p.xn_ss, 4, t_blk), xo,
+                                                      (uint32_t)r * xn_row, 0);
+              if (p.tanhy)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(zs[r]), rows_from(tyb0, p.ty_ss, 4, t_blk), yo,
+                                                      (uint32_t)r * ty_row, 0);
             }
           }
         }
@@ -438,7 +498,13 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
         }
         __syncthreads();
         s = L.carry[l];
-        for (int q = 0; q < wave; ++q) s = __builtin_fmaf(L.wA[q][l], s, L.wB[q][l]);
+        for (int q = 0; q < wave; ++q) {
+          s = __builtin_fmaf(L.wA[q][l], s, L.wB[q][l]);
+          if constexpr (FIXED) {
+            // the carried state at a tile boundary (token t_blk + (q+1) GPW R)
+            if ((t_blk - t_chunk + (q + 1) * GPW * R) % p.clamp_tile == 0) s = __builtin_amdgcn_fmed3f(s, -1.0f, 1.0f);
+          }
+        }
         s = __builtin_fmaf(eA, s, eB);
       }
       // Replay, store bf16(s), proxy gradient.
@@ -450,13 +516,13 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
           if (FULL || r < n_valid) {
             s = __builtin_fmaf(mu, s, w[r]);
             const float so = __builtin_amdgcn_fmed3f(s, -1.0f, 1.0f);
-            const float ov[1] = {(float)(__bf16)so};
+            const float ov[1] = {FIXED ? so : (float)(__bf16)so};
             // default cache policy: the 32-byte pieces that the workgroups of
             // one XCD store into a 128-byte line merge in its L2 before they
             // are written (non-temporal stores reached HBM as partial lines:
             // 1.84x the output bytes)
             __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ov[0]), orr, ovo, (uint32_t)r * o_row, 0);
-            if ((FULL && r + 1 < R) || r0 + r + 1 < len) {
+            if (!FIXED && ((FULL && r + 1 < R) || r0 + r + 1 < len)) {
               const float err = u[r + 1] - so;
               const float gv = err * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-3.0f * kLog2e * __builtin_fabsf(err)));
               const float uu = u[r], u2 = uu + uu;
@@ -478,13 +544,21 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
         replay(std::true_type{});
       else
         replay(std::false_type{});
+      if constexpr (FIXED) {
+        // the clamped state after token S-1, from the run that holds it
+        if (p.ema_final && lane_ok && n_valid > 0 && r0 + n_valid == len)
+          p.ema_final[(int64_t)b * p.final_sb + d] = __builtin_amdgcn_fmed3f(s, -1.0f, 1.0f);
+      }
       if (len > kBlockTok) {
         // The next block of this chunk starts from this block's end state
         // (a one-block chunk has no next block: the carry restarts at 0).
         __syncthreads();   // all reads of the carry and the wave maps done
         if (g == kV10Groups - 1) {
           // state after the block's last valid token (invalid tokens are skipped)
-          L.carry[l] = s;
+          float cs = s;
+          if constexpr (FIXED)
+            if ((t_blk - t_chunk + kBlockTok) % p.clamp_tile == 0) cs = __builtin_amdgcn_fmed3f(cs, -1.0f, 1.0f);
+          L.carry[l] = cs;
         }
         __syncthreads();
       }
@@ -492,6 +566,7 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
       for (int r = 0; r <= R; ++r) xcur[r] = xnxt[r];
     }
 
+    if constexpr (FIXED) continue;   // no proxy gradient, no Lion
     // Reduce the proxy gradient over the runs (a fixed butterfly inside each
     // wave, reduce-scattered over the coefficients, then the waves in
     // order), then Lion.
@@ -515,7 +590,16 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
     __syncthreads();
   }
 
-  if (tid < KP * LW) {
+  if constexpr (FIXED) {
+    // No tokens: the state passes through unclamped, as the reference's
+    // carry does when its tile loop runs zero times.
+    if (p.S == 0 && p.ema_final && tid < LW && lg * LW + tid < p.hd) {
+      const int jj = lg * LW + tid;
+      p.ema_final[(int64_t)b * p.final_sb + h * p.hd + jj] =
+          p.ema_init ? p.ema_init[(int64_t)b * p.init_sb + h * p.hd + jj] : 0.0f;
+    }
+  }
+  if (!FIXED && tid < KP * LW) {
     const int k = tid / LW, ll = tid % LW, jj = lg * LW + ll;
     if (jj < p.hd && k < p.K) {
       const size_t o = (((size_t)b * p.H + h) * p.K + k) * p.hd + jj;
@@ -525,20 +609,20 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const V10P
   }
 }
 
-template <typename XT, bool LUT, int LW>
-hipError_t launch_w(const V10Params& p, int kpad, hipStream_t stream) {
+template <typename XT, bool LUT, int LW, bool FIXED, typename P>
+hipError_t launch_w(const P& p, int kpad, hipStream_t stream) {
   const unsigned grid = (unsigned)(p.B * p.H * p.n_lg);
   if (kpad == 4)
-    hipLaunchKernelGGL((v10_chunked_kernel<XT, 4, LUT, LW>), dim3(grid), dim3(kV10Groups * LW), 0, stream, p);
+    hipLaunchKernelGGL((v10_chunked_kernel<XT, 4, LUT, LW, FIXED, P>), dim3(grid), dim3(kV10Groups * LW), 0, stream, p);
   else
-    hipLaunchKernelGGL((v10_chunked_kernel<XT, 8, LUT, LW>), dim3(grid), dim3(kV10Groups * LW), 0, stream, p);
+    hipLaunchKernelGGL((v10_chunked_kernel<XT, 8, LUT, LW, FIXED, P>), dim3(grid), dim3(kV10Groups * LW), 0, stream, p);
   return hipGetLastError();
 }
 
-template <typename XT, bool LUT>
-hipError_t launch_x(const V10Params& p, int kpad, hipStream_t stream) {
-  if (p.lanes == 8) return launch_w<XT, LUT, 8>(p, kpad, stream);
-  if (p.lanes == 16) return launch_w<XT, LUT, 16>(p, kpad, stream);
+template <typename XT, bool LUT, bool FIXED, typename P>
+hipError_t launch_x(const P& p, int kpad, hipStream_t stream) {
+  if (p.lanes == 8) return launch_w<XT, LUT, 8, FIXED>(p, kpad, stream);
+  if (p.lanes == 16) return launch_w<XT, LUT, 16, FIXED>(p, kpad, stream);
   return hipErrorInvalidValue;
 }
 
@@ -549,8 +633,15 @@ int v10_lanes(int64_t B, int64_t H, int64_t hd) {
 }
 
 hipError_t launch_v10(const V10Params& p, int x_dtype, bool use_lut, int kpad, hipStream_t stream) {
-  if (x_dtype == 0) return use_lut ? launch_x<float, true>(p, kpad, stream) : launch_x<float, false>(p, kpad, stream);
-  return use_lut ? launch_x<__bf16, true>(p, kpad, stream) : launch_x<__bf16, false>(p, kpad, stream);
+  if (x_dtype == 0)
+    return use_lut ? launch_x<float, true, false>(p, kpad, stream) : launch_x<float, false, false>(p, kpad, stream);
+  return use_lut ? launch_x<__bf16, true, false>(p, kpad, stream) : launch_x<__bf16, false, false>(p, kpad, stream);
+}
+
+hipError_t launch_v10_fixed(const V10FixedParams& p, int x_dtype, bool use_lut, int kpad, hipStream_t stream) {
+  if (x_dtype == 0)
+    return use_lut ? launch_x<float, true, true>(p, kpad, stream) : launch_x<float, false, true>(p, kpad, stream);
+  return use_lut ? launch_x<__bf16, true, true>(p, kpad, stream) : launch_x<__bf16, false, true>(p, kpad, stream);
 }
 
 }  // namespace osm

@@ -7,6 +7,9 @@
                         whose backward is ``cheby_ema_backward``).
 ``v10_chunked_ttt``     the reference's full path: online TTT over chunks with
                         an inline Lion update, in one launch.
+``cheby_ema_lut_forward`` the fixed-coefficient LUT/Clenshaw forward of the
+                        reference's _fused_clenshaw_ema_kernel (x_norm,
+                        tanh_y, out and the carried state), in one launch.
 
 All run on the current torch stream of the input's device and never
 synchronise the host.  Inputs are not modified.  There is no CPU path: a
@@ -576,6 +579,93 @@ def v10_chunked_ttt(x: torch.Tensor, coeffs: torch.Tensor, momentum: torch.Tenso
     if save_for_backward:
         return out, c_out, m_out, z, hist
     return out, c_out, m_out
+
+
+def _rows_dest(t: torch.Tensor | None, shape, dev, name: str) -> torch.Tensor | None:
+    """A caller's [B,S,D] or [B,D] fp32 output with lane stride 1, or None."""
+    if t is None:
+        return None
+    if t.shape != torch.Size(shape) or t.dtype != torch.float32 or t.device != dev or t.stride(-1) != 1:
+        raise ValueError(f"{name} must be a {tuple(shape)} float32 tensor on {dev} with lane stride 1")
+    return t
+
+
+def cheby_ema_lut_forward(x: torch.Tensor, coeffs: torch.Tensor, *, n_heads: int, ema_momentum: float = 0.9,
+                          ema_init: torch.Tensor | None = None, use_lut: bool = True, lut: torch.Tensor | None = None,
+                          clamp_tile: int = 128, out: torch.Tensor | None = None,
+                          x_norm: torch.Tensor | None = None, tanh_y: torch.Tensor | None = None,
+                          ema_final: torch.Tensor | None = None, want_x_norm: bool = True,
+                          want_tanh_y: bool = True):
+    """The reference's _fused_clenshaw_ema_kernel (sdpc_kernel.py:988-1209)
+    through osm_cheby_ema_lut_fwd: per lane, x_norm = softsign(x) (x as
+    given, NaN read as 0), y = LUT or Clenshaw series of the fixed
+    coefficients, tanh_y = tanh(clamp((0.98 - 0.06 h/H) y, -4, 4)), and the
+    EMA s = mu s + (1 - mu) tanh_y from ema_init, out = clamp(s, -1, 1), with
+    the carried state clamped every ``clamp_tile`` tokens (the kernel's
+    BLOCK_S).  x [B,S,D] fp32|bf16, coeffs [B,H,K<=8,hd], ema_init [B,D] or
+    None (0).  ``lut`` is the [8,256] table (the module's own by default).
+    Returns (out, x_norm, tanh_y, ema_final) fp32; x_norm / tanh_y are None
+    when not wanted and no buffer is given.  ``out``, ``x_norm``, ``tanh_y``
+    and ``ema_final`` may be caller buffers (lane stride 1)."""
+    lib = nat.load()
+    if not isinstance(x, torch.Tensor) or x.dim() != 3:
+        raise ValueError("x must be a [B,S,D] tensor")
+    if x.device.type != "cuda":
+        raise RuntimeError("orthossm_amd runs on a ROCm GPU only; x is on " + str(x.device))
+    dev = x.device
+    B, S, D = x.shape
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        x = x.float()
+    if x.stride(2) != 1:
+        x = x.contiguous()
+    c = coeffs.to(device=dev, dtype=torch.float32)
+    H = n_heads
+    if c.dim() != 4 or c.shape[0] != B or c.shape[1] != H or H * c.shape[3] != D:
+        raise ValueError(f"coeffs must be [B,H,K,hd] matching x {tuple(x.shape)} and n_heads={H}")
+    K, hd = c.shape[2], c.shape[3]
+    if not 1 <= K <= 8:
+        raise ValueError(f"the fused Clenshaw/LUT forward takes 1 to 8 coefficients, got {K}")
+    if c.stride(3) != 1:
+        c = c.contiguous()
+    if use_lut:
+        lut = (v10_tables(dev, H, K)[0] if lut is None
+               else lut.to(device=dev, dtype=torch.float32).reshape(LUT_TERMS, LUT_POINTS).contiguous())
+    init = None
+    if ema_init is not None:
+        init = ema_init.to(device=dev, dtype=torch.float32).reshape(B, D)
+        if init.stride(1) != 1:
+            init = init.contiguous()
+    out = _rows_dest(out, (B, S, D), dev, "out")
+    if out is None:
+        out = torch.empty((B, S, D), device=dev, dtype=torch.float32)
+    x_norm = _rows_dest(x_norm, (B, S, D), dev, "x_norm")
+    if x_norm is None and want_x_norm:
+        x_norm = torch.empty((B, S, D), device=dev, dtype=torch.float32)
+    tanh_y = _rows_dest(tanh_y, (B, S, D), dev, "tanh_y")
+    if tanh_y is None and want_tanh_y:
+        tanh_y = torch.empty((B, S, D), device=dev, dtype=torch.float32)
+    ema_final = _rows_dest(ema_final, (B, D), dev, "ema_final")
+    if ema_final is None:
+        ema_final = torch.empty((B, D), device=dev, dtype=torch.float32)
+    a = nat.LutFwdArgs()
+    a.abi_version = nat.ABI_VERSION
+    a.flags = nat.V10_USE_LUT if use_lut else 0
+    a.B, a.S, a.H, a.hd, a.K, a.clamp_tile = B, S, H, hd, K, int(clamp_tile)
+    a.x, a.x_dtype, a.x_stride_b, a.x_stride_s = x.data_ptr(), _dtype_code(x.dtype), x.stride(0), x.stride(1)
+    a.coeffs, a.c_stride_b, a.c_stride_h, a.c_stride_k = c.data_ptr(), c.stride(0), c.stride(1), c.stride(2)
+    a.lut = lut.data_ptr() if use_lut else None
+    a.ema_momentum = float(ema_momentum)
+    if init is not None:
+        a.ema_init, a.init_stride_b = init.data_ptr(), init.stride(0)
+    a.out, a.out_stride_b, a.out_stride_s = out.data_ptr(), out.stride(0), out.stride(1)
+    if x_norm is not None:
+        a.x_norm, a.xn_stride_b, a.xn_stride_s = x_norm.data_ptr(), x_norm.stride(0), x_norm.stride(1)
+    if tanh_y is not None:
+        a.tanh_y, a.ty_stride_b, a.ty_stride_s = tanh_y.data_ptr(), tanh_y.stride(0), tanh_y.stride(1)
+    a.ema_final, a.final_stride_b = ema_final.data_ptr(), ema_final.stride(0)
+    nat.check(lib.osm_cheby_ema_lut_fwd(ctypes.byref(a), ctypes.c_void_p(_current_stream(dev))))
+    keep = (x, c, lut, init)  # noqa: F841  (alive until the launch is queued)
+    return out, x_norm, tanh_y, ema_final
 
 
 def _v10_backward(x, out, z, hist, grad_out, n_heads, ema_momentum, chunk, need_coeffs):

@@ -32,8 +32,10 @@ precision_tests.py:33, ortho_diagnostics.py:174): the spectral coefficient
 initialisation ``init_chebyshev_coefficients``, the complexity gate module
 ``GatedComplexityPredictor``, the LUT accessor ``get_chebyshev_lut`` with
 ``LUT_TABLE_SIZE`` and ``MAX_DEGREE``, and ``MULTI_SCALE_LAMBDA``.  The
-reference's Triton kernel objects (``_fused_clenshaw_ema_kernel``) have no
-counterpart: their launches are the C ABI's entry points.
+one kernel object a caller launches directly, ``_fused_clenshaw_ema_kernel``
+(precision_tests.py:33, 61-73: ``kernel[grid](pointers, sizes, strides,
+BLOCK_HD=..., BLOCK_S=..., USE_LUT=...)``), is a launcher with the same
+launch syntax and argument list over ``osm_cheby_ema_lut_fwd``.
 """
 from __future__ import annotations
 
@@ -43,8 +45,8 @@ import threading
 import torch
 import torch.nn as nn
 
-from .ops import (LUT_POINTS, LUT_TERMS, V10_LION_LAMBDA, cheby_ema, cheby_ema_forward, chebyshev_lut_table,
-                  head_momentum, v10_chunked_ttt, v10_full_path)
+from .ops import (LUT_POINTS, LUT_TERMS, V10_LION_LAMBDA, cheby_ema, cheby_ema_forward, cheby_ema_lut_forward,
+                  chebyshev_lut_table, head_momentum, v10_chunked_ttt, v10_full_path)
 
 # Points of the full path's half-table LUT and the number of Chebyshev terms
 # it holds (sdpc_kernel.py:58-59).
@@ -209,3 +211,102 @@ def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_m
 
 
 apply_cheby_rkv_core = apply_cheby_rkv_v10
+
+
+class _FusedClenshawEmaLauncher:
+    """``_fused_clenshaw_ema_kernel[grid](...)`` with the reference's argument
+    list (sdpc_kernel.py:988-1005): pointer arguments are tensors, written in
+    place (XNorm, TanhY, EMAOut, FinalState) as the Triton kernel writes
+    through them.  The launch runs ``osm_cheby_ema_lut_fwd`` on the current
+    stream; BLOCK_S is the interval at which the carried state is clamped,
+    as the kernel's tile carry does (sdpc_kernel.py:1193-1200), and BLOCK_HD
+    only shapes the grid, which must be the reference's
+    (B * n_heads * ceil(head_dim / BLOCK_HD),).  Strides must be those of the
+    tensors passed (the kernel reads through them; other strides raise)."""
+
+    _ARGS = ("X_ptr", "C_ptr", "LUT_ptr", "XNorm_ptr", "TanhY_ptr", "EMAOut_ptr", "InitState_ptr", "FinalState_ptr",
+             "seq_len", "total_dim", "head_dim", "n_heads", "degree", "lut_size", "momentum",
+             "stride_xb", "stride_xs", "stride_xd",
+             "stride_cb", "stride_ch", "stride_cdeg", "stride_cd",
+             "stride_lk", "stride_lt",
+             "stride_xnb", "stride_xns", "stride_xnd",
+             "stride_tyb", "stride_tys", "stride_tyd",
+             "stride_ob", "stride_os", "stride_od",
+             "stride_sb", "stride_sd",
+             "BLOCK_HD", "BLOCK_S", "USE_LUT")
+
+    def __getitem__(self, grid):
+        def launch(*args, **kwargs):
+            return self._launch(grid, args, kwargs)
+        return launch
+
+    def _launch(self, grid, args, kwargs):
+        if len(args) > len(self._ARGS):
+            raise TypeError(f"_fused_clenshaw_ema_kernel takes {len(self._ARGS)} arguments, got {len(args)}")
+        a = dict(zip(self._ARGS, args))
+        for k, v in kwargs.items():
+            if k not in self._ARGS:
+                raise TypeError(f"_fused_clenshaw_ema_kernel got an unexpected argument {k!r}")
+            if k in a:
+                raise TypeError(f"_fused_clenshaw_ema_kernel got multiple values for {k!r}")
+            a[k] = v
+        missing = [k for k in self._ARGS if k not in a]
+        if missing:
+            raise TypeError(f"_fused_clenshaw_ema_kernel is missing {missing}")
+        x, c, lut = a["X_ptr"], a["C_ptr"], a["LUT_ptr"]
+        S, D, hd, H, K = (int(a[k]) for k in ("seq_len", "total_dim", "head_dim", "n_heads", "degree"))
+        if H * hd != D or x.dim() != 3 or x.shape[1] < S or x.shape[2] != D:
+            raise ValueError(f"x {tuple(x.shape)} does not match seq_len={S}, n_heads={H}, head_dim={hd}")
+        B = x.shape[0]
+        block_hd = int(a["BLOCK_HD"])
+        g = tuple(grid(dict(a)) if callable(grid) else grid)
+        if g[:1] != (B * H * math.ceil(hd / block_hd),) or any(int(v) != 1 for v in g[1:]):
+            raise ValueError(f"grid {g} is not the kernel's (B * n_heads * cdiv(head_dim, BLOCK_HD),)")
+        if int(a["lut_size"]) != LUT_TABLE_SIZE:
+            raise ValueError(f"lut_size={a['lut_size']}: the table has {LUT_TABLE_SIZE} points")
+        if not 1 <= K <= MAX_DEGREE or c.shape[2] < K:
+            raise ValueError(f"degree={K} outside [1, {MAX_DEGREE}] or beyond the coefficients' {c.shape[2]}")
+
+        def strides_of(t, names):
+            got = tuple(int(a[n]) for n in names)
+            if got != tuple(t.stride()):
+                raise NotImplementedError(f"{names[0][:-1]}*: strides {got} differ from the tensor's {tuple(t.stride())}")
+
+        strides_of(x, ("stride_xb", "stride_xs", "stride_xd"))
+        strides_of(c, ("stride_cb", "stride_ch", "stride_cdeg", "stride_cd"))
+        strides_of(lut, ("stride_lk", "stride_lt"))
+        rows = {"XNorm_ptr": ("stride_xnb", "stride_xns", "stride_xnd"),
+                "TanhY_ptr": ("stride_tyb", "stride_tys", "stride_tyd"),
+                "EMAOut_ptr": ("stride_ob", "stride_os", "stride_od")}
+        for name, st in rows.items():
+            strides_of(a[name], st)
+        init, fin = a["InitState_ptr"], a["FinalState_ptr"]
+        strides_of(init, ("stride_sb", "stride_sd"))
+        strides_of(fin, ("stride_sb", "stride_sd"))
+
+        def dest(t, shape):
+            # the kernel writes through the caller's pointer: a lane-stride-1
+            # view is written directly, anything else via a copy afterwards
+            v = t[:, :shape[1]] if len(shape) == 3 else t
+            return v if v.stride(-1) == 1 and v.dtype == torch.float32 else None
+
+        xn, ty, out = a["XNorm_ptr"], a["TanhY_ptr"], a["EMAOut_ptr"]
+        shp = (B, S, D)
+        d_xn, d_ty, d_out, d_fin = dest(xn, shp), dest(ty, shp), dest(out, shp), dest(fin, (B, D))
+        r_out, r_xn, r_ty, r_fin = cheby_ema_lut_forward(
+            x[:, :S], c[:, :, :K], n_heads=H, ema_momentum=float(a["momentum"]), ema_init=init[:, :D],
+            use_lut=bool(a["USE_LUT"]), lut=lut, clamp_tile=int(a["BLOCK_S"]), out=d_out, x_norm=d_xn,
+            tanh_y=d_ty, ema_final=d_fin)
+        if d_out is None:
+            out[:, :S].copy_(r_out)
+        if d_xn is None:
+            xn[:, :S].copy_(r_xn)
+        if d_ty is None:
+            ty[:, :S].copy_(r_ty)
+        if d_fin is None:
+            fin.copy_(r_fin)
+
+
+# The reference's fused Clenshaw + EMA kernel object (sdpc_kernel.py:988),
+# launched as ``_fused_clenshaw_ema_kernel[grid](...)`` (precision_tests.py:61-73).
+_fused_clenshaw_ema_kernel = _FusedClenshawEmaLauncher()

@@ -36,7 +36,7 @@ def test_every_declared_function_is_exported():
 
 
 @pytest.mark.parametrize("cls,cname", [(nat.ChebyArgs, "osm_cheby_args"), (nat.BwdArgs, "osm_cheby_bwd_args"),
-                                      (nat.V10Args, "osm_v10_args")])
+                                      (nat.V10Args, "osm_v10_args"), (nat.LutFwdArgs, "osm_lut_fwd_args")])
 def test_struct_layout_matches_ctypes(cls, cname):
     fields = [f for f, _ in cls._fields_]
     prog = ['#include <stdio.h>', '#include <stddef.h>', '#include "osm.h"', "int main(void){",
@@ -266,6 +266,48 @@ def test_v10_argument_errors(kw, code):
     lib = nat.load()
     assert lib.osm_v10_chunked_ttt(ctypes.byref(_v10(**kw)), None) == code
     assert lib.osm_last_error() != b""
+
+
+def _lut(**kw):
+    a = nat.LutFwdArgs()
+    a.abi_version = nat.ABI_VERSION
+    a.flags = nat.V10_USE_LUT
+    a.B, a.S, a.H, a.hd, a.K, a.clamp_tile = 2, 256, 8, 8, 4, 128
+    a.x = a.out = a.coeffs = a.lut = 0x10000
+    a.x_stride_b = a.out_stride_b = 256 * 64
+    a.x_stride_s = a.out_stride_s = 64
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(abi_version=3), -1),
+    (dict(flags=0x10), -1),
+    (dict(K=9), -2),
+    (dict(K=0), -2),
+    (dict(clamp_tile=8), -2),          # the carried state is clamped between waves of 16 tokens
+    (dict(clamp_tile=40), -2),
+    (dict(x_dtype=5), -3),
+    (dict(lut=0), -1),                 # LUT mode needs the table
+    (dict(out=0), -1),
+    (dict(out_stride_s=32), -4),       # rows overlap
+    (dict(x_norm=0x10000, xn_stride_b=256 * 64, xn_stride_s=32), -4),
+    (dict(tanh_y=0x10002, ty_stride_b=256 * 64, ty_stride_s=64), -4),   # misaligned
+    (dict(ema_final=0x10000, final_stride_b=32), -4),                   # final rows overlap
+    (dict(x_stride_s=1 << 22), -4),    # 257 rows over 2 GiB
+])
+def test_lut_fwd_argument_errors(kw, code):
+    lib = nat.load()
+    assert lib.osm_cheby_ema_lut_fwd(ctypes.byref(_lut(**kw)), None) == code
+    assert lib.osm_last_error() != b""
+    assert lib.osm_cheby_ema_lut_fwd(None, None) == -1
+
+
+def test_lut_fwd_empty_batch_is_a_no_op():
+    # B = 0 returns before any pointer is looked at (no GPU work)
+    lib = nat.load()
+    assert lib.osm_cheby_ema_lut_fwd(ctypes.byref(_lut(B=0, x=0, out=0, coeffs=0)), None) == 0
 
 
 def test_error_messages_are_thread_local():

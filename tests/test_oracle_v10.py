@@ -216,3 +216,101 @@ def test_full_path_backward_nan_gives_nan_grad_x():
                             ema_momentum=0.9, chunk=256)
     assert np.isnan(gx[0, 3, 1]) and np.isfinite(np.delete(gx.reshape(-1), 3 * 4 + 1)).all()
     assert np.isfinite(gc).all()
+
+
+# The fused Clenshaw + EMA kernel (_fused_clenshaw_ema_kernel,
+# sdpc_kernel.py:988-1209), restated by V.fused_clenshaw_ema.
+
+def test_clenshaw8_is_the_chebyshev_series_of_all_eight_terms():
+    u = rng.uniform(-1, 1, 30)
+    for K in (5, 6, 8):
+        c = rng.standard_normal((30, K))
+        got = V.clenshaw8_series(c, u)
+        want = np.array([npcheb.chebval(u[j], c[j]) for j in range(30)])
+        np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("K,use_lut", [(3, False), (4, False), (6, False), (8, False), (8, True), (2, True)])
+def test_fused_clenshaw_ema_series_tanh_and_scan(K, use_lut):
+    B, S, H, hd = 2, 300, 2, 4
+    D = H * hd
+    x = rng.standard_normal((B, S, D)).astype(np.float32)
+    c = rng.standard_normal((B, H, K, hd)) / 2
+    xn, ty, out, fin = V.fused_clenshaw_ema(x, c, n_heads=H, ema_momentum=0.93, use_lut=use_lut)
+    u = np.sign(x) * (1.0 - 1.0 / (1.0 + np.maximum(np.abs(x.astype(np.float64)), np.float32(1e-7))))
+    np.testing.assert_allclose(xn, u, rtol=1e-15)
+    cl = c.transpose(0, 1, 3, 2).reshape(B, 1, D, K)
+    if use_lut:
+        lut = V.chebyshev_lut()
+        p = V.lut_series(cl, np.abs(u), np.sign(u), lut)
+        # the LUT series is within its interpolation bound of the exact series
+        exact = np.stack([[npcheb.chebval(u[b, :, d], cl[b, 0, d]) for d in range(D)] for b in range(B)], 0)
+        assert np.abs(p - exact.transpose(0, 2, 1)).max() < 1e-3
+    else:
+        terms = cl if K > 4 else cl[..., :4]
+        p = np.stack([[npcheb.chebval(u[b, :, d], terms[b, 0, d]) for d in range(D)] for b in range(B)], 0)
+        p = p.transpose(0, 2, 1)
+    gamma = np.repeat(0.98 - 0.06 * np.arange(H) / H, hd)
+    np.testing.assert_allclose(ty, np.tanh(np.clip(gamma * p, -4, 4)), atol=1e-12)
+    # zero initial state: every clamp is the identity and the EMA is lfilter's
+    ema = scipy.signal.lfilter([0.07], [1.0, -0.93], ty, axis=1)
+    np.testing.assert_allclose(out, ema, atol=1e-12)
+    np.testing.assert_allclose(fin, ema[:, -1], atol=1e-12)
+
+
+def test_fused_clenshaw_ema_clamps_the_carry_at_tile_boundaries():
+    B, S, H, hd = 1, 200, 1, 3
+    x = rng.standard_normal((B, S, H * hd)).astype(np.float32)
+    c = rng.standard_normal((B, H, 4, hd)) / 4
+    mu = 0.9999
+    init = np.array([[5.0, -3.0, 0.5]])
+    _, ty, out, fin = V.fused_clenshaw_ema(x, c, n_heads=H, ema_momentum=mu, ema_init=init, block_s=64)
+    assert np.all(np.abs(out) <= 1.0)
+    # inside the first tile the state runs from the unclamped init: out is
+    # the clipped EMA of lfilter with that initial condition
+    first = scipy.signal.lfilter([1 - mu], [1.0, -mu], ty[:, :64], axis=1, zi=mu * init[:, None, :])[0]
+    np.testing.assert_allclose(out[:, :64], np.clip(first, -1, 1), atol=1e-12)
+    # from the second tile on, the carry is the clipped state
+    second = scipy.signal.lfilter([1 - mu], [1.0, -mu], ty[:, 64:128], axis=1,
+                                  zi=mu * np.clip(first[:, -1:, :], -1, 1))[0]
+    np.testing.assert_allclose(out[:, 64:128], np.clip(second, -1, 1), atol=1e-12)
+    # a tile as long as the sequence never clamps the carry: only the output
+    _, _, out_1, _ = V.fused_clenshaw_ema(x, c, n_heads=H, ema_momentum=mu, ema_init=init, block_s=256)
+    whole = scipy.signal.lfilter([1 - mu], [1.0, -mu], ty, axis=1, zi=mu * init[:, None, :])[0]
+    np.testing.assert_allclose(out_1, np.clip(whole, -1, 1), atol=1e-12)
+    assert np.abs(out_1 - out).max() > 1e-3      # lane 0 starts at 5: the carry clamp binds
+    # |init| <= 1: the tile size does not matter
+    init2 = np.array([[0.9, -1.0, 0.2]])
+    a = V.fused_clenshaw_ema(x, c, n_heads=H, ema_momentum=mu, ema_init=init2, block_s=32)
+    b = V.fused_clenshaw_ema(x, c, n_heads=H, ema_momentum=mu, ema_init=init2, block_s=512)
+    np.testing.assert_allclose(a[2], b[2], atol=1e-13)
+    np.testing.assert_allclose(fin, out[:, -1], atol=0)
+
+
+def test_fused_clenshaw_ema_special_values_and_empty_sequence():
+    # token t of every lane holds special value t
+    vals = np.array([np.nan, 0.0, np.inf, -np.inf, -0.0, 3e38, 1e-30, -2.0], np.float32)
+    x = np.repeat(vals.reshape(1, 8, 1), 8, axis=2)
+    c = np.ones((1, 1, 8, 8)) * 0.1
+    xn, ty, out, fin = V.fused_clenshaw_ema(x, c, n_heads=1)
+    assert np.all(np.isfinite(out)) and np.all(np.isfinite(xn)) and np.all(np.isfinite(ty))
+    tiny = 1.0 - 1.0 / (1.0 + np.float64(np.float32(1e-7)))
+    # NaN reads as 0 (x_norm = +tiny) and gives tanh_y = 0; +-Inf give +-1
+    assert xn[0, 0, 0] == pytest.approx(tiny, rel=1e-12) and ty[0, 0, 0] == 0.0
+    assert xn[0, 1, 0] == pytest.approx(tiny, rel=1e-12) and xn[0, 4, 0] == pytest.approx(tiny, rel=1e-12)
+    assert xn[0, 2, 0] == 1.0 and xn[0, 3, 0] == -1.0 and xn[0, 6, 0] == pytest.approx(tiny, rel=1e-12)
+    init = rng.standard_normal((1, 8)) * 3
+    _, _, out0, fin0 = V.fused_clenshaw_ema(np.zeros((1, 0, 8), np.float32), c, n_heads=1, ema_init=init)
+    assert out0.shape == (1, 0, 8)
+    np.testing.assert_array_equal(fin0, init)            # unclamped, as the kernel's untouched carry
+
+
+def test_fused_clenshaw_ema_matches_the_full_path_output_on_one_chunk():
+    # precision_tests.py P1: on one chunk with a zero state, the full path's
+    # output before Lion is this kernel's on bf16 x, up to the bf16 rounding
+    B, S, H, hd, K = 2, 256, 8, 8, 4
+    x = rng.standard_normal((B, S, H * hd)).astype(np.float32)
+    c = rng.standard_normal((B, H, K, hd))
+    full, _, _ = V.v10_full(x, c, np.zeros_like(c), n_heads=H, chunk_size=512)
+    _, _, out, _ = V.fused_clenshaw_ema(V.bf16_round(x), c, n_heads=H, ema_momentum=0.9)
+    np.testing.assert_array_equal(full, V.bf16_round(out.astype(np.float32)))
