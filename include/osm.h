@@ -4,7 +4,7 @@
  * One fused operator, per batch b, token t, head h, lane j (d = h*hd + j):
  *
  *   u = x / (1 + |x|)                               softsign
- *   p = sum_{k<K} c[b,h,k,j] T_k(u)                 Clenshaw, K <= 16 (<= 8 for the TTT)
+ *   p = sum_{k<K} c[b,h,k,j] T_k(u)                 Clenshaw, K <= 32 (<= 8 for the TTT)
  *   z = tanh(damping[h] * p)                        (z = 0 where x is NaN, or u = 0
  *                                                    with OSM_FLAG_NAN_ZERO_U)
  *   s[t] = lam[b,t,h] s[t-1] + (1 - lam[b,t,h]) z   s[-1] = ema_init (0 if NULL)
@@ -78,7 +78,7 @@ extern "C" {
 #endif
 
 #define OSM_ABI_VERSION 2
-#define OSM_MAX_K 16      /* coefficients per lane: forward and backward */
+#define OSM_MAX_K 32      /* coefficients per lane: forward and backward */
 #define OSM_MAX_K_TTT 8   /* coefficients per lane: the TTT gradient */
 
 typedef enum osm_dtype { OSM_F32 = 0, OSM_BF16 = 1 } osm_dtype;

@@ -13,7 +13,7 @@ import threading
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libosm.so")
 
 ABI_VERSION = 2
-MAX_K = 16       # forward and backward
+MAX_K = 32       # forward and backward
 MAX_K_TTT = 8    # the TTT gradient
 MAX_K_V10 = 8    # the full path's series (coefficients past it pass through)
 F32 = 0

@@ -79,7 +79,7 @@ int check_args(const osm_cheby_args* a, Geometry* geo, int op, bool shapes_only 
   if (a->out_dtype != OSM_F32 && a->out_dtype != OSM_BF16)
     return fail(OSM_E_DTYPE, "out_dtype %d unsupported", a->out_dtype);
   geo->dyn = a->g != nullptr;
-  geo->kpad = a->K <= 4 ? 4 : (a->K <= 8 ? 8 : 16);
+  geo->kpad = a->K <= 4 ? 4 : (a->K <= 8 ? 8 : (a->K <= 16 ? 16 : 32));
   geo->empty = a->B == 0 || a->S == 0;
   const int xs = a->x_dtype == OSM_F32 ? 4 : 2;
   const int os = a->out_dtype == OSM_F32 ? 4 : 2;

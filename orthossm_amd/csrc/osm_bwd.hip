@@ -413,6 +413,11 @@ hipError_t launch_k(const BwdParams& bp, int tile, int kpad, hipStream_t stream)
     if (bp.zs) return hipErrorInvalidValue;
     return launch_all<BwdTileCheb, DYN, false, XT, OT, 16>(bp, stream);
   }
+  if (kpad == 32) {
+    if (tile != BwdTileCheb32::TILE) return hipErrorInvalidValue;
+    if (bp.zs) return hipErrorInvalidValue;
+    return launch_all<BwdTileCheb32, DYN, false, XT, OT, 32>(bp, stream);
+  }
   using G = BwdTile;
   if (tile != G::TILE) return hipErrorInvalidValue;
   if (bp.zs) {
@@ -437,12 +442,14 @@ hipError_t launch_dt(const BwdParams& bp, int x_dtype, int out_dtype, int tile, 
 
 }  // namespace
 
-int bwd_tile_tokens(bool, int kpad) { return kpad > kMonoMaxK ? BwdTileCheb::TILE : BwdTile::TILE; }
+int bwd_tile_tokens(bool, int kpad) {
+  return kpad > 16 ? BwdTileCheb32::TILE : (kpad > kMonoMaxK ? BwdTileCheb::TILE : BwdTile::TILE);
+}
 
 size_t bwd_slot_bytes(int n_lb, int n_tiles) { return fwd_workspace_bytes(n_lb, n_tiles, kLanes, true); }
 
 size_t bwd_workspace_bytes(int n_lb, int n_tiles, int K) {
-  const size_t kpad = K <= 4 ? 4 : (K <= 8 ? 8 : 16);
+  const size_t kpad = K <= 4 ? 4 : (K <= 8 ? 8 : (K <= 16 ? 16 : 32));
   const size_t slots = (bwd_slot_bytes(n_lb, n_tiles) + 255) / 256 * 256;
   return slots + (size_t)n_lb * n_tiles * kpad * kLanes * sizeof(float);
 }

@@ -337,8 +337,8 @@ hipError_t launch_g(const FwdParams& p, int kpad, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// The one-lane geometry also serves the Chebyshev form (kpad 16); K <= 4
-// runs with kpad 8 there (zero coefficients), one instantiation fewer.
+// The one-lane geometry also serves the Chebyshev form (kpad 16 and 32);
+// K <= 4 runs with kpad 8 there (zero coefficients), one instantiation fewer.
 template <bool DYN, typename XT, typename OT>
 hipError_t launch_generic(const FwdParams& p, int kpad, hipStream_t stream) {
   using G = FwdTileGeneric;
@@ -347,6 +347,8 @@ hipError_t launch_generic(const FwdParams& p, int kpad, hipStream_t stream) {
     hipLaunchKernelGGL((cheby_ema_fwd_kernel<G, DYN, XT, OT, 8>), dim3(grid), dim3(G::THREADS), 0, stream, p);
   else if (kpad == 16)
     hipLaunchKernelGGL((cheby_ema_fwd_kernel<G, DYN, XT, OT, 16>), dim3(grid), dim3(G::THREADS), 0, stream, p);
+  else if (kpad == 32)
+    hipLaunchKernelGGL((cheby_ema_fwd_kernel<G, DYN, XT, OT, 32>), dim3(grid), dim3(G::THREADS), 0, stream, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

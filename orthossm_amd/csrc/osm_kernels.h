@@ -107,8 +107,11 @@ int ttt_tile_tokens(bool dyn, int x_dtype);
 // tokens 114.3, 28 tokens 118.2, 32 tokens 114.2; 8-token runs are slower
 // (185 us).
 using BwdTile = TileGeo<1, 8, 24, 64, 2>;   // 192 tokens
-// More than 8 coefficients (Chebyshev form, kpad 16): 12-token runs.
+// More than 8 coefficients (Chebyshev form, kpad 16): 12-token runs; more
+// than 16 (kpad 32): 4-token runs, room for 3 x 32 coefficient and gradient
+// registers.
 using BwdTileCheb = TileGeo<1, 8, 12, 64, 2>;   // 96 tokens
+using BwdTileCheb32 = TileGeo<1, 8, 4, 64, 2>;  // 32 tokens
 int bwd_tile_tokens(bool dyn, int kpad);
 
 // Upper bound on polls of one look-back word (each poll is a device-scope

@@ -55,7 +55,7 @@ MAX_DEGREE: int = LUT_TERMS
 # Per-head Lion forget factors of the full path, heads 0..7 (sdpc_kernel.py:1416).
 MULTI_SCALE_LAMBDA = list(V10_LION_LAMBDA)
 # Most Chebyshev coefficients the fixed-coefficient (fast) path evaluates.
-MAX_FAST_TERMS = 16
+MAX_FAST_TERMS = 32
 
 _lut_lock = threading.Lock()
 _lut_by_device: dict = {}
@@ -199,7 +199,7 @@ def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_m
         # The reference's PyTorch fast path evaluates any number of terms
         # (sdpc_kernel.py:1751-1776); its Triton kernels and its engine
         # (max_degree <= 8) stop at eight.  Here the fixed-coefficient kernels
-        # take up to 16 (more than 8 by Clenshaw).
+        # take up to 32 (more than 8 by Clenshaw).
         raise ValueError(f"the fast path supports at most {MAX_FAST_TERMS} Chebyshev coefficients, "
                          f"got {coeffs.shape[2]}")
     damping, lam = _fast_constants(H, x.device, ema_momentum)

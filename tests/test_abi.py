@@ -86,7 +86,9 @@ def test_workspace_bytes_formula():
     assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 128 * 64 * 8
     a.x_stride_s, a.hd = 512, 62              # D = 496: 8 lane-blocks per row, the last one partial
     assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 128 * 64 * 8
-    a.hd, a.K = 64, 17
+    a.hd, a.K = 64, 17                        # the Chebyshev form up to 32 terms: the same geometry
+    assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 2048 + 32 * 128 * 64 * 8
+    a.K = 33
     assert lib.osm_workspace_bytes(ctypes.byref(a), 0) == 0
 
 
@@ -147,14 +149,14 @@ def test_coefficient_limits_per_entry_point():
         assert lib.osm_workspace_bytes(ctypes.byref(_args(K=K)), nat.OP_BWD) > 0
         assert lib.osm_workspace_bytes(ctypes.byref(_args(K=K)), nat.OP_TTT) == 0     # the TTT takes K <= 8
         assert b"TTT" in lib.osm_last_error()
-    assert nat.MAX_K == 16 and nat.MAX_K_TTT == 8
+    assert nat.MAX_K == 32 and nat.MAX_K_TTT == 8
 
 
 @pytest.mark.parametrize("kw,code", [
     (dict(abi_version=99), -1),
     (dict(flags=0x100), -1),
     (dict(K=0), -2),
-    (dict(K=17), -2),
+    (dict(K=33), -2),
     (dict(hd=0), -2),
     (dict(H=0), -2),
     (dict(S=-1), -2),
@@ -200,6 +202,10 @@ def test_bwd_workspace_bytes_formula():
     a.K = 12
     slots = (2048 + 32 * 171 * 64 * 16 + 255) // 256 * 256
     assert lib.osm_workspace_bytes(ctypes.byref(a), nat.OP_BWD) == slots + 32 * 171 * 16 * 64 * 4
+    # more than 16: 32-token tiles (512 at S=16384), 32 padded
+    a.K = 20
+    slots = (2048 + 32 * 512 * 64 * 16 + 255) // 256 * 256
+    assert lib.osm_workspace_bytes(ctypes.byref(a), nat.OP_BWD) == slots + 32 * 512 * 32 * 64 * 4
     assert lib.osm_workspace_bytes(ctypes.byref(a), 3) == 0
     assert b"osm_op" in lib.osm_last_error()
 
@@ -223,7 +229,7 @@ def _bwd(**kw):
     ({}, dict(gx_stride_b=512), -4),          # batches overlap
     (dict(out=0), {}, -1),                    # the clamp mask needs the saved output
     (dict(out=0, flags=nat.FLAG_NO_CLAMP), {}, -5),   # ... unless there is no clamp: reaches the workspace check
-    (dict(K=17), {}, -2),
+    (dict(K=33), {}, -2),
     (dict(K=9), dict(z_saved=0x20000, z_stride_b=16384 * 512, z_stride_s=512), -1),   # the saved z needs K <= 8
 ])
 def test_bwd_argument_errors(akw, bkw, code):
@@ -313,13 +319,13 @@ def test_lut_fwd_empty_batch_is_a_no_op():
 def test_error_messages_are_thread_local():
     import threading
     lib = nat.load()
-    a = _args(K=17)
+    a = _args(K=33)
     assert lib.osm_cheby_ema_fwd(ctypes.byref(a), None, 0, None) == -2
     seen = []
     t = threading.Thread(target=lambda: seen.append(lib.osm_last_error()))
     t.start()
     t.join()
-    assert seen == [b""] and b"K=17" in lib.osm_last_error()
+    assert seen == [b""] and b"K=33" in lib.osm_last_error()
 
 
 def _doc_struct(name):

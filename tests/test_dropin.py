@@ -41,10 +41,10 @@ def test_cpu_tensor_raises():
         apply_cheby_rkv_v10(x, c, None, n_heads=4)
 
 
-def test_fast_path_rejects_more_than_sixteen_coefficients():
+def test_fast_path_rejects_more_than_thirty_two_coefficients():
     # the reference's PyTorch fast path takes any number of terms; the
-    # fixed-coefficient kernels here take up to 16
+    # fixed-coefficient kernels here take up to 32
     x = torch.randn(1, 16, 32)
-    c = torch.randn(1, 4, 17, 8)
-    with pytest.raises(ValueError, match="at most 16"):
+    c = torch.randn(1, 4, 33, 8)
+    with pytest.raises(ValueError, match="at most 32"):
         apply_cheby_rkv_v10(x, c, torch.zeros_like(c), n_heads=4, seq_threshold=384)

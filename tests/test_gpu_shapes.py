@@ -1,6 +1,6 @@
 """Layouts and series lengths outside the fast geometries, against the
 float64 oracle: head sizes that are not multiples of 4 (down to 1), rows off
-4-element boundaries (strided views of wider tensors), and 9..16 Chebyshev
+4-element boundaries (strided views of wider tensors), and 9..32 Chebyshev
 coefficients (the Clenshaw form), for the forward (one-lane geometry), the
 backward and, up to 8 coefficients, the TTT gradient.  The reference's
 PyTorch fast path takes any head size and any number of terms
@@ -26,6 +26,9 @@ pytestmark = pytest.mark.gpu
     (1, 2000, 2, 64, 16, True, torch.float32),        # 16 terms, dynamic lambda
     (2, 600, 3, 10, 9, False, torch.bfloat16),        # bf16 in and out, 9 terms
     (1, 8 * 128 * 8 + 5, 1, 3, 16, False, torch.float32),   # crosses 8 look-back checkpoints
+    (2, 900, 4, 16, 24, False, torch.float32),        # 24 terms (kpad 32)
+    (1, 1500, 2, 32, 32, True, torch.float32),        # 32 terms, dynamic lambda
+    (2, 400, 2, 8, 17, False, torch.bfloat16),        # bf16, 17 terms
 ])
 def test_forward_generic_layouts(dev, B, S, H, hd, K, dyn, dtype):
     inp = inputs(B, S, H, hd, K, seed=S + hd + K, dynamic=dyn, dtype=dtype)
@@ -39,7 +42,7 @@ def test_forward_generic_layouts(dev, B, S, H, hd, K, dyn, dtype):
     # that grows with K (the b_k grow with the number of terms): ~1e-6 up to
     # 8 terms, ~3e-6 measured at 16.  The spec's 1e-5 relative to the
     # largest magnitude is checked unchanged.
-    atol = 1e-6 if K <= 8 else 4e-6
+    atol = 1e-6 if K <= 8 else (4e-6 if K <= 16 else 8e-6)
     if dtype == torch.bfloat16:
         err = np.abs(out.float().cpu().numpy() - want)
         assert err.max() <= 2e-2 and np.all(err <= 2.0 ** -8 * np.abs(want) + atol)
@@ -48,7 +51,7 @@ def test_forward_generic_layouts(dev, B, S, H, hd, K, dyn, dtype):
     assert_close_fp32(fin.cpu(), wfin, atol=atol, what="ema_final")
 
 
-@pytest.mark.parametrize("offset,K", [(1, 8), (3, 4), (2, 13)])
+@pytest.mark.parametrize("offset,K", [(1, 8), (3, 4), (2, 13), (1, 32)])
 def test_forward_rows_off_four_element_boundaries(dev, offset, K):
     # x and out are views starting `offset` elements into wider rows (row
     # stride D + 5): neither the pointers nor the strides are 4-aligned.
@@ -65,7 +68,7 @@ def test_forward_rows_off_four_element_boundaries(dev, offset, K):
     cheby_ema_forward(xw, d["coeffs"], d["damping"], d["lam"], out=outv)
     torch.cuda.synchronize()
     want, _ = oracle_forward(inp)
-    assert_close_fp32(outv.cpu(), want, atol=1e-6 if K <= 8 else 4e-6)
+    assert_close_fp32(outv.cpu(), want, atol=1e-6 if K <= 8 else (4e-6 if K <= 16 else 8e-6))
     # the columns around the view are untouched
     assert torch.isnan(out_wide[:, :, :offset]).all() and torch.isnan(out_wide[:, :, offset + D:]).all()
 
@@ -75,6 +78,8 @@ def test_forward_rows_off_four_element_boundaries(dev, offset, K):
     (1, 1100, 2, 7, 12, True),
     (2, 500, 4, 16, 16, False),
     (1, 96 * 16 * 3 + 7, 1, 64, 10, False),       # 96-token tiles: crosses 3 look-back checkpoints
+    (2, 500, 4, 16, 32, False),                   # 32 terms: 32-token tiles
+    (1, 700, 2, 7, 20, True),                     # 20 terms, hd = 7, dynamic lambda
 ])
 def test_backward_generic_layouts(dev, B, S, H, hd, K, dyn):
     inp = inputs(B, S, H, hd, K, seed=S + K, dynamic=dyn)
@@ -131,3 +136,21 @@ def test_drop_in_fast_path_with_twelve_terms_and_odd_heads(dev):
     gx, gc, _ = O.backward(*args, go.double().numpy(), nan_policy="zero_u", out_saved=out.detach().cpu().numpy())
     assert_close_grad(x.grad.cpu(), gx, what="grad_x")
     assert_close_grad(c.grad.cpu(), gc, what="grad_coeffs")
+
+
+def test_dropin_fast_path_with_32_terms(dev):
+    # the reference's fast path evaluates any number of terms
+    # (sdpc_kernel.py:1751-1776): 32 here, forward and gradients
+    B, S, H, hd, K = 2, 300, 4, 16, 32
+    inp = inputs(B, S, H, hd, K, seed=97)
+    x = inp["x"].to(dev).requires_grad_(True)
+    c = inp["coeffs"].to(dev).requires_grad_(True)
+    mom = torch.zeros_like(c)
+    out, c_out, _ = apply_cheby_rkv_v10(x, c, mom, n_heads=H, ema_momentum=0.9)
+    (out * torch.linspace(-1, 1, S, device=dev).view(1, S, 1)).sum().backward()
+    torch.cuda.synchronize()
+    assert c_out is c and torch.isfinite(x.grad).all() and torch.isfinite(c.grad).all()
+    damping = 0.98 - 0.06 * np.arange(H) / H
+    want, _ = O.forward(inp["x"].double().numpy(), inp["coeffs"].numpy(), damping, np.full(H, 0.9),
+                        nan_policy="zero_u")
+    assert_close_fp32(out.detach().cpu(), want, atol=8e-6)
