@@ -177,7 +177,11 @@ def apply_cheby_rkv_v10(x, coeffs, momentum_buf, n_heads=4, base_lr=0.005, ema_m
     returns (out [B,S,D] fp32, coeffs fp32, momentum_buf fp32 or None).
     ``ema_momentum`` may also be a one-element tensor on the device, read
     there by the kernels (the reference takes a Python float, which its
-    engine obtains with a host synchronisation, sdpc_engine.py:209)."""
+    engine obtains with a host synchronisation, sdpc_engine.py:209).
+    ``lion_max_norm`` and ``use_bf16`` are accepted and have no effect, as
+    in the reference: its megakernel takes ``max_norm`` (sdpc_kernel.py:1907,
+    passed at 2324) and never reads it, and the full path rounds x to bf16
+    whatever ``use_bf16`` says (2385)."""
     B, S, D = x.shape
     if coeffs.dtype != torch.float32:
         coeffs = coeffs.float()

@@ -112,6 +112,12 @@ def test_dropin_full_path(dev):
     torch.cuda.synchronize()
     assert out.dtype == torch.float32 and cn.dtype == torch.float32
     compare(out, cn, mn, oracle(x, c, m, n_heads=H, gate_global=gate.numpy(), dynamic_lambda=gate.numpy()))
+    # lion_max_norm and use_bf16 change nothing, as in the reference's full
+    # path (its megakernel never reads max_norm; x is rounded to bf16 anyway)
+    out2, cn2, mn2 = apply_cheby_rkv_v10(x.to(dev), c.to(dev), m.to(dev), n_heads=H, seq_threshold=384,
+                                         gate_global=gate.to(dev), dynamic_lambda=gate.to(dev),
+                                         lion_max_norm=1e-3, use_bf16=True)
+    assert torch.equal(out2, out) and torch.equal(cn2, cn) and torch.equal(mn2, mn)
     # below the threshold the same call takes the fixed-coefficient path
     out_s, c_s, m_s = apply_cheby_rkv_v10(x[:, :300].to(dev), c.to(dev), m.to(dev), n_heads=H, seq_threshold=384)
     assert torch.equal(c_s.cpu(), c)
