@@ -219,9 +219,7 @@ cheby_ema_bwd_kernel(const BwdParams bp) {
     uint32_t sg = 0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      float t[1];
-      BufVec<float, 1>::load(a.g, a.vg, sg, t);
-      lamv[r] = t[0];
+      lamv[r] = load_f32_shared(a.g, a.vg, sg);   // a line of g serves every lane-block of the row
       sg = next_off(sg, a.sg);
     }
   }

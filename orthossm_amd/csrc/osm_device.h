@@ -263,6 +263,14 @@ struct BufVec<__bf16, 1> {
   }
 };
 
+// One fp32 value with the default cache policy, for data that several
+// workgroups of one XCD read at different times (the coefficients, g, x lines
+// split between workgroups): with the non-temporal hint the L2 may drop the
+// line before the others have read it.
+__device__ __forceinline__ float load_f32_shared(Rsrc r, uint32_t vo, uint32_t so) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
+}
+
 template <>
 struct BufVec<__bf16, 2> {
   static __device__ __forceinline__ void load(Rsrc r, uint32_t vo, uint32_t so, float (&v)[2]) {

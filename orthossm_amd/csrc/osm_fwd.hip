@@ -163,9 +163,9 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     for (int i = 0; i < kGL; ++i) {
       const int idx = q.tid + i * G::THREADS;
       const int t = idx % G::TILE, hh = idx / G::TILE;
-      float v[1];
-      BufVec<float, 1>::load(a.g, idx < n_gl ? (uint32_t)((t * p.g_ss + (h0 + hh) * p.g_sh) * 4) : kOffOOB, 0, v);
-      glv[i] = v[0];
+      // (each 128-byte line of g, four tokens of every head, is read by all
+      // the lane-blocks of the row)
+      glv[i] = load_f32_shared(a.g, idx < n_gl ? (uint32_t)((t * p.g_ss + (h0 + hh) * p.g_sh) * 4) : kOffOOB, 0);
       lhv[i] = p.lam[min(h0 + hh, p.H - 1)];   // (idx >= n_gl: not used)
     }
   }
@@ -192,10 +192,9 @@ cheby_ema_fwd_kernel(const FwdParams p) {
     for (int i = 0; i < kGL; ++i)
       if (q.tid + i * G::THREADS < n_gl) lam_of(q.tid + i * G::THREADS, glv[i], lhv[i]);
     for (int idx = q.tid + kGL * G::THREADS; idx < n_gl; idx += G::THREADS) {   // small heads only
-      float v[1];
       const int t = idx % G::TILE, hh = idx / G::TILE;
-      BufVec<float, 1>::load(a.g, (uint32_t)((t * p.g_ss + (h0 + hh) * p.g_sh) * 4), 0, v);
-      lam_of(idx, v[0], p.lam[h0 + hh]);
+      const float gv = load_f32_shared(a.g, (uint32_t)((t * p.g_ss + (h0 + hh) * p.g_sh) * 4), 0);
+      lam_of(idx, gv, p.lam[h0 + hh]);
     }
   }
   __syncthreads();

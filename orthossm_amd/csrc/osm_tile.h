@@ -102,10 +102,9 @@ __device__ __forceinline__ MonoLoad<KP, G> mono_issue(const FwdParams& p, const 
       // out-of-range offset): a branch here would make the compiler convert
       // each value inside it and so wait for every load on the spot, before
       // the caller's bulk loads are issued.
+      // (every tile of the lane-block, all on one XCD, reads them)
       const int k = j + 2 * i;
-      float v[1];
-      BufVec<float, 1>::load(a.c, k < p.K ? vc : kOffOOB, (uint32_t)k * a.sc, v);
-      m.cm[n][i] = v[0];
+      m.cm[n][i] = load_f32_shared(a.c, k < p.K ? vc : kOffOOB, (uint32_t)k * a.sc);
     }
     m.kap[n] = kTwoLog2e * p.damping[h];
   }

@@ -291,9 +291,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
     uint32_t sg = 0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      float gv[1];
-      BufVec<float, 1>::load(a.g, a.vg, sg, gv);
-      lamv[r] = gv[0];
+      lamv[r] = load_f32_shared(a.g, a.vg, sg);   // a line of g serves every lane-block of the row
       sg = next_off(sg, a.sg);
     }
   }
@@ -305,9 +303,7 @@ cheby_ema_ttt_kernel(const FwdParams p) {
   if (last_run) {
     BufVec<XT, LPT>::load(a.x, a.vx, (uint32_t)R * a.sx, x_after);
     if constexpr (DYN) {
-      float gv[1];
-      BufVec<float, 1>::load(a.g, a.vg, (uint32_t)R * a.sg, gv);
-      g_after = gv[0];
+      g_after = load_f32_shared(a.g, a.vg, (uint32_t)R * a.sg);
     }
   }
 

@@ -54,6 +54,21 @@ __device__ __forceinline__ float to_bf16_value<__bf16>(float v) {
   return v;   // loaded from bf16 already
 }
 
+// One x value with the default cache policy (not non-temporal): each
+// 128-byte line of x is read by the 128 / (4 LW) workgroups of one XCD,
+// which reach it at different times (with the non-temporal hint, x was read
+// 1.05-1.15 times over from HBM).
+template <typename XT>
+__device__ __forceinline__ float load_x(Rsrc r, uint32_t vo, uint32_t so);
+template <>
+__device__ __forceinline__ float load_x<float>(Rsrc r, uint32_t vo, uint32_t so) {
+  return load_f32_shared(r, vo, so);
+}
+template <>
+__device__ __forceinline__ float load_x<__bf16>(Rsrc r, uint32_t vo, uint32_t so) {
+  return __uint_as_float((unsigned)__builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0) << 16);
+}
+
 // The megakernel's softsign on a bf16 value: |u| and sign(u); NaN reads as 0.
 __device__ __forceinline__ void v10_softsign(float xb, float& absu, float& sgn) {
   const float xs = xb == xb ? xb : 0.0f;
@@ -293,9 +308,7 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const P p)
     uint32_t so = 0;
 #pragma unroll
     for (int r = 0; r <= R; ++r) {
-      float t[1];
-      BufVec<XT, 1>::load(xr, vo_, so, t);
-      dst[r] = t[0];
+      dst[r] = load_x<XT>(xr, vo_, so);
       so = next_off(so, x_row);
     }
   };
