@@ -337,12 +337,14 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const P p)
       }
     }
   };
-  // Token 0 of every run is prepared ahead of its block: for a chunk's first
-  // block while the previous chunk's Lion update runs (a window in which
-  // the other waves wait), so that its table reads are off the chunk's
-  // chain.  Measured at the configs[1] shape, bit-identical: one token
-  // ahead 152.6-153.7 against 153.9-155.0 us; two and three tokens ahead
-  // 162.6 and 170.2 us (their reads outgrow the window).
+  // Token 0 of every run is prepared ahead of its block, so that its table
+  // reads are off the chunk's chain: for a chunk's first block by the first
+  // wave of each SIMD while it waits for the second at the reduction
+  // barrier, and by the others while wave 0 applies Lion.  Measured at the
+  // configs[1] shape, bit-identical: one token ahead, all waves during
+  // Lion, 152.6-153.7 against 153.9-155.0 us; two and three tokens ahead
+  // 162.6 and 170.2 us (their reads outgrow the window); the first waves
+  // before the barrier 150.4-150.6 against 151.1-151.6 us.
   TokPre f0;
   if (!FIXED || n_chunks > 0) load_run(xcur, 0);   // (the fixed forward takes S = 0: no rows)
   // Wait for these rows here, once.  Without it the compiler, merging this
@@ -610,6 +612,10 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const P p)
     // wave, reduce-scattered over the coefficients, then the waves in
     // order), then Lion.
     store_run_sums<LW, KP>(gc, L.ws[wave], l, gw);
+    // The first wave of each SIMD reaches the barrier early: it prepares its
+    // token 0 of the next chunk here, the others while Lion runs.
+    const bool early = wave < V10Lds<LW>::NW / 2;
+    if (early && ch + 1 < n_chunks) prep(xcur[0], f0, true);
     __syncthreads();
     if (tid < KP * LW) {
       const int k = tid / LW, ll = tid % LW;
@@ -627,7 +633,7 @@ __global__ void __launch_bounds__(kV10Groups * LW) v10_chunked_kernel(const P p)
       }
     }
     // token 0 of the next chunk's first block, while Lion runs
-    if (ch + 1 < n_chunks) prep(xcur[0], f0, true);
+    if (!early && ch + 1 < n_chunks) prep(xcur[0], f0, true);
     __syncthreads();
   }
 
